@@ -1,0 +1,344 @@
+#!/usr/bin/env python3
+"""Benchmark of the blockwise-causal attention path on one MI355X.
+
+Headline (BASELINE.json ``metric``): block-causal attention TFLOP/s and its
+fraction of the dense bf16 MFMA peak at the Wan-5B shape, and ms per 83-token
+chunk. A *step* is one 83-token chunk through the path for all 30 layers of
+Wan2.2-TI2V-5B (config C1): per layer, QK-RMSNorm+RoPE of the chunk's q/k and
+blockwise-causal attention over that layer's 1,245 cached keys plus the 83
+new ones. The 30 per-layer caches (16.3 MB each, 489 MB in all) exceed the
+256 MB MALL, so the cache really streams from HBM. Inputs are synthetic,
+seeded (C1 recipe), resident in HBM before timing. Steps are replayed from a
+HIP graph; K steps are timed with synchronisation on both sides.
+
+``value`` = 30 x 1.354 GFLOP (visible pairs only) / step time. Alongside:
+``roofline`` for the attention kernel at C1 (HBM-bound: algorithmic bytes
+per launch / event-timed launch duration), ``cpu_baseline`` (the torch fp32
+oracle timed on this host), and ``extra`` with the prologue, the fused
+prologue+append, and attention at C2 (8K prefill, MFMA-bound), C3 and C4.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "dexter-labs_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_BF16_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 dense bf16 FLOP/clk/CU
+PEAK_HBM_GBPS = 8000.0
+LAYERS_5B = 30
+DEFAULT_METRIC = "block-causal attn TFLOP/s + % bf16 MFMA peak @Wan-5B; ms per 83-token chunk"
+
+
+def _metric_name() -> str:
+    try:
+        return json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+    except Exception:
+        return DEFAULT_METRIC
+
+
+def _profile_traffic() -> dict | None:
+    """HBM bytes per attention launch at C1 from the committed rocprof counter summary."""
+    path = ROOT / "profiles" / "attn_fwd_C1_hbm_traffic.md"
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return {"bytes": float(m.group(1)), "source": str(path.relative_to(ROOT))} if m else None
+
+
+def _per_layer_inputs(inp, device, layers: int, cache_len: int):
+    """Per-layer chunk activations and per-layer caches holding the rotated history."""
+    import torch
+
+    import dexter_amd.ops as ops
+
+    cfg = inp.cfg
+    c = cache_len
+    q, k, v = inp.q.to(device), inp.k.to(device), inp.v.to(device)
+    qw, kw = inp.q_weight.to(device), inp.k_weight.to(device)
+    cos, sin = inp.cos.to(device), inp.sin.to(device)
+    base = torch.zeros(2, cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim, dtype=cfg.dtype,
+                       device=device)
+    _, kr = ops.qk_norm_rope(q[:, :c], k[:, :c], qw, kw, cos[:c], sin[:c])
+    ops.kv_cache_append(base, kr, v[:, :c], 0)
+    caches = [base.clone() for _ in range(layers)]
+    chunk = [tuple(t[:, c:].clone() for t in (q, k, v)) for _ in range(layers)]
+    tables = (cos[c:].contiguous(), sin[c:].contiguous())
+    torch.cuda.synchronize()
+    return caches, chunk, (qw, kw), tables
+
+
+def run_headline(args, device):
+    import time
+
+    import torch
+
+    import dexter_amd.ops as ops
+    from dexter_amd.bench import harness
+    from dexter_amd.bench.workloads import CONFIGS, make_inputs
+
+    cfg = CONFIGS["C1"]
+    L = args.layers
+    c = cfg.cache_lens[0]
+    inp = make_inputs(cfg)
+    caches, chunk, (qw, kw), (cos, sin) = _per_layer_inputs(inp, device, L, c)
+
+    def step():
+        for layer in range(L):
+            qi, ki, vi = chunk[layer]
+            qc, kc = ops.qk_norm_rope(qi, ki, qw, kw, cos, sin)
+            ops.blockwise_causal_attention(qc, kc, vi, kv_cache=caches[layer], cache_len=c)
+
+    # Eager (Python dispatch per op) for reference, then the graph that is timed.
+    for _ in range(max(1, args.warmup)):
+        step()
+    eager_ms = harness.wall_time_ms(step, reps=max(3, args.steps // 5))
+    graph = harness.capture(step)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Attention alone, per launch (event-timed graph of L launches).
+    rot = []
+    for layer in range(L):
+        qi, ki, vi = chunk[layer]
+        rot.append(ops.qk_norm_rope(qi, ki, qw, kw, cos, sin) + (vi,))
+    attn_graph = harness.capture(lambda: [
+        ops.blockwise_causal_attention(rot[i][0], rot[i][1], rot[i][2], kv_cache=caches[i],
+                                       cache_len=c) for i in range(L)])
+    attn_ms = harness.event_time_ms(attn_graph.replay, reps=max(5, args.steps // 2)) / L
+    pro_graph = harness.capture(lambda: [ops.qk_norm_rope(chunk[i][0], chunk[i][1], qw, kw, cos,
+                                                          sin) for i in range(L)])
+    pro_ms = harness.event_time_ms(pro_graph.replay, reps=max(5, args.steps // 2)) / L
+
+    # Fused prologue + append (the priming pass's form), per launch.
+    def prime():
+        for i in range(L):
+            ops.qk_norm_rope_append(chunk[i][0], chunk[i][1], chunk[i][2], qw, kw, cos, sin,
+                                    caches[i], c)
+    prime_graph = harness.capture(prime)
+    prime_ms = harness.event_time_ms(prime_graph.replay, reps=max(5, args.steps // 2)) / L
+
+    flops = cfg.flops()
+    attn_bytes = cfg.bytes()
+    tok = cfg.q_len * cfg.heads * cfg.head_dim * 2
+    pro_bytes = 4 * tok + 2 * cfg.heads * cfg.head_dim * 2 + 2 * cfg.q_len * cfg.head_dim // 2 * 4
+    value = L * flops / (ms_per_step * 1e-3) / 1e12
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    traffic = _profile_traffic()
+    return {
+        "ms_per_step": ms_per_step,
+        "value": value,
+        "eager_ms_per_step": eager_ms,
+        "attn_ms": attn_ms,
+        "roofline": {
+            "bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_GBPS,
+            "traffic": traffic["bytes"] if traffic else None,
+            "kernel": "attn_fwd_kernel<3,128,bf16> + attn_combine_kernel (split-KV), C1",
+            "algorithmic_bytes_per_launch": attn_bytes,
+            "launch_us": attn_ms * 1e3,
+            "tflops": flops / (attn_ms * 1e-3) / 1e12,
+        },
+        "prologue": {"us": pro_ms * 1e3, "gbps": pro_bytes / (pro_ms * 1e-3) / 1e9,
+                     "bytes": pro_bytes},
+        "prologue_append_fused": {"us": prime_ms * 1e3,
+                                  "gbps": (pro_bytes + 2 * tok) / (prime_ms * 1e-3) / 1e9,
+                                  "bytes": pro_bytes + 2 * tok},
+        "inputs": inp,
+    }
+
+
+def run_config(name: str, device, reps: int) -> dict:
+    """Attention alone at one config: event-timed per call, TFLOP/s, GB/s."""
+    import torch
+
+    import dexter_amd.ops as ops
+    from dexter_amd.bench import harness
+    from dexter_amd.bench.workloads import CONFIGS, block_tensor, make_inputs
+
+    cfg = CONFIGS[name]
+    inp = make_inputs(cfg)
+    bb = block_tensor(cfg, device)
+    if name == "C4":
+        lens = list(cfg.cache_lens)
+        b, h, d = cfg.batch, cfg.heads, cfg.head_dim
+        cache = torch.zeros(2, b, max(lens), h, d, dtype=cfg.dtype)
+        kq = torch.zeros(b, cfg.q_len, h, d, dtype=cfg.dtype)
+        vq = torch.zeros_like(kq)
+        for i, c in enumerate(lens):
+            cache[0, i, :c], cache[1, i, :c] = inp.k[i, :c], inp.v[i, :c]
+            kq[i], vq[i] = inp.k[i, c:c + cfg.q_len], inp.v[i, c:c + cfg.q_len]
+        q, kq, vq, cache = (t.to(device) for t in (inp.q, kq, vq, cache))
+
+        def call():
+            ops.blockwise_causal_attention_varlen(q, kq, vq, kv_cache=cache, cache_lens=lens,
+                                                  block_boundaries=bb)
+    else:
+        c = cfg.cache_lens[0]
+        q, k, v = inp.q.to(device), inp.k.to(device), inp.v.to(device)
+        qw, kw = inp.q_weight.to(device), inp.k_weight.to(device)
+        cos, sin = inp.cos.to(device), inp.sin.to(device)
+        qr, kr = ops.qk_norm_rope(q, k, qw, kw, cos, sin)
+        cache = None
+        if c:
+            cache = torch.zeros(2, cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim,
+                                dtype=cfg.dtype, device=device)
+            ops.kv_cache_append(cache, kr[:, :c], v[:, :c], 0)
+        qc, kc, vc = qr[:, c:].contiguous(), kr[:, c:].contiguous(), v[:, c:].contiguous()
+        del q, k, qr, kr
+
+        def call():
+            ops.blockwise_causal_attention(qc, kc, vc, kv_cache=cache, cache_len=c,
+                                           block_boundaries=bb)
+    graph = harness.capture(call)
+    ms = harness.event_time_ms(graph.replay, reps=reps)
+    return {
+        "us": ms * 1e3,
+        "tflops": cfg.flops() / (ms * 1e-3) / 1e12,
+        "pct_mfma_peak": 100 * cfg.flops() / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "gbps": cfg.bytes() / (ms * 1e-3) / 1e9,
+        "pct_hbm_peak": 100 * cfg.bytes() / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+        "gflop": cfg.flops() / 1e9,
+        "bytes": cfg.bytes(),
+    }
+
+
+def run_cpu_baseline(inp, budget_s: float) -> dict:
+    """The torch fp32 oracle on this host's cores, C1 attention per layer (a bounded sample)."""
+    import platform as pyplatform
+
+    import torch
+
+    from dexter_amd.bench import harness
+    from oracle import attention as oatt
+    from oracle import rope as orope
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    cfg = inp.cfg
+    c = cfg.cache_lens[0]
+    rq, rk = orope.qk_norm_rope(inp.q, inp.k, inp.q_weight, inp.k_weight, inp.cos, inp.sin, 1e-6)
+    cache = torch.stack((rk[:, :c], inp.v[:, :c]))
+    qc, kc, vc = rq[:, c:], rk[:, c:], inp.v[:, c:]
+
+    def call():
+        oatt.blockwise_causal_attention(qc, kc, vc, cache, c, None, None)
+
+    ms, runs = harness.cpu_median_ms(call, budget_s)
+    return {
+        "value": cfg.flops() / (ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"C1 attention (one layer: 83 q x 1,328 keys x 24 heads), torch fp32 oracle "
+                   f"(oracle/attention.py), median of {runs} calls in ~{budget_s:.0f} s; "
+                   f"ms per 30-layer chunk = {LAYERS_5B * ms:.2f}"),
+        "ms_per_call": ms,
+        "cpu": pyplatform.processor() or pyplatform.machine(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=LAYERS_5B)
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU work for the cpu_baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip C2/C3/C4")
+    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4"], default=None,
+                    help="time one config's attention only (for profiling runs)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="first run a plain device copy of this size (counter calibration)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); attention heads shard across GPUs with no collective, "
+              "so the one-GPU number is the per-GPU figure.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    device = torch.device("cuda", 0)
+    import dexter_amd.ops  # noqa: F401
+    from dexter_amd.ops.gfx950 import _lib
+
+    _lib.load()  # fail loudly if the HIP library is missing
+
+    if args.copy_mb:
+        n = args.copy_mb * (1 << 20)
+        src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy calibration: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
+        del src, dst
+
+    if args.only:
+        res = run_config(args.only, device, reps=max(10, args.steps))
+        print(json.dumps({"only": args.only, **res}), flush=True)
+        return 0
+
+    head = run_headline(args, device)
+    print(f"headline done: {head['ms_per_step']:.4f} ms/step", file=sys.stderr, flush=True)
+    extra = {"eager_ms_per_step": head["eager_ms_per_step"], "prologue_C1": head["prologue"],
+             "prologue_append_fused_C1": head["prologue_append_fused"]}
+    if not args.no_extra:
+        for name, reps in (("C2", 20), ("C3", 20), ("C4", 50)):
+            extra[name] = run_config(name, device, reps)
+            print(f"{name} done: {extra[name]['us']:.1f} us", file=sys.stderr, flush=True)
+    cpu = None if args.no_cpu else run_cpu_baseline(head["inputs"], args.cpu_budget)
+
+    line = {
+        "metric": _metric_name(),
+        "value": head["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded C1 recipe; random q/k/v, norm weights 1+0.1N(0,1), theta=1e4 RoPE)",
+        "config": {"workload": "C1 Wan-5B closed-loop chunk: 83 queries over 1,245 cached + 83 "
+                               "new keys, 24 heads x 128, x 30 layers (prologue + attention)",
+                   "layers": args.layers, "q_len": 83, "cache_len": 1245, "heads": 24,
+                   "head_dim": 128, "batch": 1},
+        "pct_mfma_peak": 100 * head["value"] / PEAK_BF16_TFLOPS,
+        "ms_per_83_token_chunk": head["ms_per_step"],
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,363 @@
+// Fused QK-RMSNorm + rotary for gfx950, optionally writing the rotated k and
+// the raw v straight into a KV-cache slot.
+//
+// Semantics follow dexter's reference op (python/dexter/ops/reference/rope.py):
+//   _rms  (:29-40)  x * rsqrt(mean(x^2 over the token's whole H*D plane) + eps)
+//                   * weight, in fp32, then rounded to the io dtype;
+//   _rope (:10-26)  out_lo = lo*c - hi*s, out_hi = lo*s + hi*c in fp32 (each
+//                   product and sum rounded separately, no fused multiply-add),
+//                   then rounded to the io dtype.
+// Keeping the reference's intermediate rounding makes this kernel agree with
+// the oracle to within the summation order of the mean.
+//
+// Work layout: one workgroup per (batch, token). A thread owns "units" of 8
+// rotary pairs: 16 consecutive elements when pairs are interleaved (2j, 2j+1),
+// or 8 elements at offset o plus 8 at o + D/2 for split-half pairs. Each unit
+// is two 16-byte loads per tensor, so the plane is read exactly once, with
+// the sum of squares reduced across the workgroup through LDS.
+#include "dx_common.h"
+
+namespace dx {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxUnits = 4;  // H*D <= kThreads * kMaxUnits * 16 = 16384
+
+template <typename W> struct Vec8;
+template <> struct Vec8<bf16_t> {
+  static __device__ __forceinline__ void load(const void* p, float (&o)[8]) {
+    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(r[i] << 16);
+      o[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Vec8<f16_t> {
+  static __device__ __forceinline__ void load(const void* p, float (&o)[8]) {
+    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = to_f32(f16_t{uint16_t(r[i] & 0xffffu)});
+      o[2 * i + 1] = to_f32(f16_t{uint16_t(r[i] >> 16)});
+    }
+  }
+};
+template <> struct Vec8<float> {
+  static __device__ __forceinline__ void load(const void* p, float (&o)[8]) {
+    f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
+    f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { o[i] = a[i]; o[4 + i] = b[i]; }
+  }
+};
+
+// Round a float to the io type and back, as ``.to(x.dtype)`` then ``.float()``.
+template <typename IO>
+__device__ __forceinline__ float round_io(float x) {
+  uint16_t b = Store<IO>::bits(x);
+  return to_f32(IO{b});
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) s += red[w];
+  return s;
+}
+
+struct RopeArgs {
+  const uint16_t* q; int64_t q_sb, q_sl, q_sh;
+  const uint16_t* k; int64_t k_sb, k_sl, k_sh;
+  const uint16_t* v; int64_t v_sb, v_sl, v_sh;
+  const void* qw; const void* kw;
+  const void* cos; int64_t cos_sl;
+  const void* sin; int64_t sin_sl;
+  uint16_t* q_out; uint16_t* k_out;
+  uint16_t* ck; uint16_t* cv; int64_t c_sb, c_ss, c_sh; int64_t start;
+  int L, H, D;
+  float eps;
+};
+
+// Element offsets (within one head) of the lo and hi halves of unit u's pairs.
+template <bool INTERLEAVED>
+__device__ __forceinline__ void unit_offsets(int unit_in_head, int D, int& lo, int& hi) {
+  if (INTERLEAVED) { lo = unit_in_head * 16; hi = lo + 8; }
+  else { lo = unit_in_head * 8; hi = lo + D / 2; }
+}
+
+template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND>
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeArgs a) {
+  __shared__ float red[2][kThreads / 64];
+  const int token = blockIdx.x;  // b * L + l
+  const int b = token / a.L, l = token % a.L;
+  const int units_per_head = a.D / 16;
+  const int n_units = a.H * units_per_head;
+  const int HD = a.H * a.D;
+
+  u32x4 qa[kMaxUnits][2], ka[kMaxUnits][2];
+  float sq = 0.f, sk = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxUnits; ++i) {
+    const int u = threadIdx.x + i * kThreads;
+    if (u < n_units) {
+      const int h = u / units_per_head, uh = u % units_per_head;
+      int lo, hi;
+      unit_offsets<INTERLEAVED>(uh, a.D, lo, hi);
+      const uint16_t* qp = a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh;
+      const uint16_t* kp = a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh;
+      qa[i][0] = *reinterpret_cast<const u32x4*>(qp + lo);
+      qa[i][1] = *reinterpret_cast<const u32x4*>(qp + hi);
+      ka[i][0] = *reinterpret_cast<const u32x4*>(kp + lo);
+      ka[i][1] = *reinterpret_cast<const u32x4*>(kp + hi);
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float x0 = to_f32(IO{uint16_t(qa[i][p][j] & 0xffffu)});
+          float x1 = to_f32(IO{uint16_t(qa[i][p][j] >> 16)});
+          float y0 = to_f32(IO{uint16_t(ka[i][p][j] & 0xffffu)});
+          float y1 = to_f32(IO{uint16_t(ka[i][p][j] >> 16)});
+          sq += x0 * x0 + x1 * x1;
+          sk += y0 * y0 + y1 * y1;
+        }
+    }
+  }
+  const float tq = block_sum(sq, red[0]);
+  const float tk = block_sum(sk, red[1]);
+  const float rq = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tq, float(HD)) + a.eps));
+  const float rk = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tk, float(HD)) + a.eps));
+
+#pragma unroll
+  for (int i = 0; i < kMaxUnits; ++i) {
+    const int u = threadIdx.x + i * kThreads;
+    if (u >= n_units) continue;
+    const int h = u / units_per_head, uh = u % units_per_head;
+    int lo, hi;
+    unit_offsets<INTERLEAVED>(uh, a.D, lo, hi);
+
+    float wq[2][8], wk[2][8];
+    Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + lo, wq[0]);
+    Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + hi, wq[1]);
+    Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + lo, wk[0]);
+    Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + hi, wk[1]);
+    // Pair index of this unit's first pair within the head.
+    const int j0 = INTERLEAVED ? uh * 8 : lo;
+    float c[8], s[8];
+    Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0, c);
+    Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0, s);
+
+    // Unpack to 16 values each: x[p][e] is element e of half p.
+    float xq[2][8], xk[2][8];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xq[p][2 * j] = to_f32(IO{uint16_t(qa[i][p][j] & 0xffffu)});
+        xq[p][2 * j + 1] = to_f32(IO{uint16_t(qa[i][p][j] >> 16)});
+        xk[p][2 * j] = to_f32(IO{uint16_t(ka[i][p][j] & 0xffffu)});
+        xk[p][2 * j + 1] = to_f32(IO{uint16_t(ka[i][p][j] >> 16)});
+      }
+    // Norm: (x * r) * w rounded to the io type, as _rms does.
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        xq[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xq[p][e], rq), wq[p][e]));
+        xk[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xk[p][e], rk), wk[p][e]));
+      }
+    // Rotate pair t (t = 0..7) and write back into the same slots.
+    float oq[2][8], ok[2][8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      // Interleaved: pair t is elements (2t, 2t+1) of the 16-element span,
+      // i.e. half t/4, elements 2(t%4) and 2(t%4)+1. Split-half: element t of
+      // half 0 against element t of half 1.
+      const int p_lo = INTERLEAVED ? t / 4 : 0, e_lo = INTERLEAVED ? 2 * (t % 4) : t;
+      const int p_hi = INTERLEAVED ? t / 4 : 1, e_hi = INTERLEAVED ? 2 * (t % 4) + 1 : t;
+      const float ql = xq[p_lo][e_lo], qh = xq[p_hi][e_hi];
+      const float kl = xk[p_lo][e_lo], kh = xk[p_hi][e_hi];
+      oq[p_lo][e_lo] = __fsub_rn(__fmul_rn(ql, c[t]), __fmul_rn(qh, s[t]));
+      oq[p_hi][e_hi] = __fadd_rn(__fmul_rn(ql, s[t]), __fmul_rn(qh, c[t]));
+      ok[p_lo][e_lo] = __fsub_rn(__fmul_rn(kl, c[t]), __fmul_rn(kh, s[t]));
+      ok[p_hi][e_hi] = __fadd_rn(__fmul_rn(kl, s[t]), __fmul_rn(kh, c[t]));
+    }
+    u32x4 pq[2], pk[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pq[p][j] = pack2<IO>(oq[p][2 * j], oq[p][2 * j + 1]);
+        pk[p][j] = pack2<IO>(ok[p][2 * j], ok[p][2 * j + 1]);
+      }
+    const int64_t obase = (int64_t(token) * a.H + h) * a.D;
+    *reinterpret_cast<u32x4*>(a.q_out + obase + lo) = pq[0];
+    *reinterpret_cast<u32x4*>(a.q_out + obase + hi) = pq[1];
+    *reinterpret_cast<u32x4*>(a.k_out + obase + lo) = pk[0];
+    *reinterpret_cast<u32x4*>(a.k_out + obase + hi) = pk[1];
+    if (APPEND) {
+      const int64_t cbase = b * a.c_sb + (a.start + l) * a.c_ss + h * a.c_sh;
+      *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = pk[0];
+      *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = pk[1];
+      const uint16_t* vp = a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
+      *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = *reinterpret_cast<const u32x4*>(vp + lo);
+      *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = *reinterpret_cast<const u32x4*>(vp + hi);
+    }
+  }
+}
+
+template <typename IO, typename W, typename TB, bool APPEND>
+hipError_t launch3(const RopeArgs& a, int tokens, bool interleaved, hipStream_t st) {
+  if (interleaved)
+    hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, true, APPEND>), dim3(tokens),
+                       dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, false, APPEND>), dim3(tokens),
+                       dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+template <typename IO, typename W, bool APPEND>
+hipError_t launch2(const RopeArgs& a, int tokens, int tdt, bool il, hipStream_t st) {
+  switch (tdt) {
+    case DX_BF16: return launch3<IO, W, bf16_t, APPEND>(a, tokens, il, st);
+    case DX_F16: return launch3<IO, W, f16_t, APPEND>(a, tokens, il, st);
+    default: return launch3<IO, W, float, APPEND>(a, tokens, il, st);
+  }
+}
+
+template <typename IO, bool APPEND>
+hipError_t launch1(const RopeArgs& a, int tokens, int wdt, int tdt, bool il, hipStream_t st) {
+  switch (wdt) {
+    case DX_BF16: return launch2<IO, bf16_t, APPEND>(a, tokens, tdt, il, st);
+    case DX_F16: return launch2<IO, f16_t, APPEND>(a, tokens, tdt, il, st);
+    default: return launch2<IO, float, APPEND>(a, tokens, tdt, il, st);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                 const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh, int io_dtype,
+                 const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
+                 const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
+                 int64_t B, int64_t L, int64_t H, int64_t D) {
+  DX_CHECK_ARG(io_dtype == DX_BF16 || io_dtype == DX_F16,
+               "qk_norm_rope: io dtype must be bf16 or f16 (got code %d)", io_dtype);
+  DX_CHECK_ARG(wdt == DX_BF16 || wdt == DX_F16 || wdt == DX_F32,
+               "qk_norm_rope: weight dtype code %d unsupported", wdt);
+  DX_CHECK_ARG(tdt == DX_BF16 || tdt == DX_F16 || tdt == DX_F32,
+               "qk_norm_rope: cos/sin dtype code %d unsupported", tdt);
+  DX_CHECK_ARG(B >= 0 && L >= 0 && H > 0 && D > 0, "qk_norm_rope: bad shape");
+  DX_CHECK_ARG(D % 16 == 0, "qk_norm_rope: head_dim %lld must be a multiple of 16",
+               (long long)D);
+  DX_CHECK_ARG(H * D <= int64_t(kThreads) * kMaxUnits * 16,
+               "qk_norm_rope: H*D = %lld exceeds %d", (long long)(H * D),
+               kThreads * kMaxUnits * 16);
+  DX_CHECK_ARG(B * L < (int64_t(1) << 31), "qk_norm_rope: too many tokens");
+  DX_CHECK_ARG(q && k && qw && kw && cos && sin && q_out && k_out,
+               "qk_norm_rope: null pointer");
+  DX_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(qw) && aligned16(kw) &&
+                   aligned16(cos) && aligned16(sin) && aligned16(q_out) && aligned16(k_out),
+               "qk_norm_rope: pointers must be 16-byte aligned");
+  DX_CHECK_ARG(q_sb % 8 == 0 && q_sl % 8 == 0 && q_sh % 8 == 0 && k_sb % 8 == 0 &&
+                   k_sl % 8 == 0 && k_sh % 8 == 0,
+               "qk_norm_rope: q/k strides must be multiples of 8 elements");
+  const int64_t tb = (tdt == DX_F32) ? 4 : 8;  // elements per 16 bytes... for alignment
+  DX_CHECK_ARG(cos_sl % tb == 0 && sin_sl % tb == 0,
+               "qk_norm_rope: cos/sin row strides must keep rows 16-byte aligned");
+  (void)tb;
+  return DX_OK;
+}
+
+}  // namespace
+}  // namespace dx
+
+using namespace dx;
+
+static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                      const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                      const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh, int io_dtype,
+                      const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
+                      const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
+                      void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                      int64_t capacity, int64_t start, int64_t B, int64_t L, int64_t H,
+                      int64_t D, float eps, int interleaved, void* stream, bool append) {
+  int rc = check_common(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, io_dtype, qw, kw, wdt, cos,
+                        cos_sl, sin, sin_sl, tdt, q_out, k_out, B, L, H, D);
+  if (rc) return rc;
+  if (append) {
+    DX_CHECK_ARG(cache && v, "qk_norm_rope_append: null cache or v");
+    DX_CHECK_ARG(start >= 0, "qk_norm_rope_append: negative start");
+    if (start + L > capacity) {
+      set_error("KV cache full: %lld + %lld > %lld", (long long)start, (long long)L,
+                (long long)capacity);
+      return DX_EFULL;
+    }
+    DX_CHECK_ARG(aligned16(cache) && aligned16(v) && c_plane % 8 == 0 && c_sb % 8 == 0 &&
+                     c_ss % 8 == 0 && c_sh % 8 == 0 && v_sb % 8 == 0 && v_sl % 8 == 0 &&
+                     v_sh % 8 == 0,
+                 "qk_norm_rope_append: cache/v must be 16-byte aligned with strides "
+                 "that are multiples of 8 elements");
+  }
+  if (B * L == 0) return DX_OK;
+  RopeArgs a{};
+  a.q = static_cast<const uint16_t*>(q); a.q_sb = q_sb; a.q_sl = q_sl; a.q_sh = q_sh;
+  a.k = static_cast<const uint16_t*>(k); a.k_sb = k_sb; a.k_sl = k_sl; a.k_sh = k_sh;
+  a.v = static_cast<const uint16_t*>(v); a.v_sb = v_sb; a.v_sl = v_sl; a.v_sh = v_sh;
+  a.qw = qw; a.kw = kw; a.cos = cos; a.cos_sl = cos_sl; a.sin = sin; a.sin_sl = sin_sl;
+  a.q_out = static_cast<uint16_t*>(q_out); a.k_out = static_cast<uint16_t*>(k_out);
+  if (append) {
+    a.ck = static_cast<uint16_t*>(cache);
+    a.cv = static_cast<uint16_t*>(cache) + c_plane;
+    a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh; a.start = start;
+  }
+  a.L = int(L); a.H = int(H); a.D = int(D); a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int tokens = int(B * L);
+  hipError_t e;
+  if (io_dtype == DX_BF16)
+    e = append ? launch1<bf16_t, true>(a, tokens, wdt, tdt, interleaved != 0, st)
+               : launch1<bf16_t, false>(a, tokens, wdt, tdt, interleaved != 0, st);
+  else
+    e = append ? launch1<f16_t, true>(a, tokens, wdt, tdt, interleaved != 0, st)
+               : launch1<f16_t, false>(a, tokens, wdt, tdt, interleaved != 0, st);
+  if (e != hipSuccess) {
+    set_error("qk_norm_rope: launch failed: %s", hipGetErrorString(e));
+    return DX_ELAUNCH;
+  }
+  return DX_OK;
+}
+
+extern "C" int dx_qk_norm_rope(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                               const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                               int io_dtype, const void* q_weight, const void* k_weight,
+                               int weight_dtype, const void* cos, int64_t cos_sl,
+                               const void* sin, int64_t sin_sl, int table_dtype, void* q_out,
+                               void* k_out, int64_t B, int64_t L, int64_t H, int64_t D,
+                               float eps, int interleaved, void* stream) {
+  return rope_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, nullptr, 0, 0, 0, io_dtype,
+                    q_weight, k_weight, weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype,
+                    q_out, k_out, nullptr, 0, 0, 0, 0, 0, 0, B, L, H, D, eps, interleaved,
+                    stream, false);
+}
+
+extern "C" int dx_qk_norm_rope_append(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k, int64_t k_sb,
+    int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    int io_dtype, const void* q_weight, const void* k_weight, int weight_dtype,
+    const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl, int table_dtype,
+    void* q_out, void* k_out, void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
+    int64_t c_sh, int64_t capacity, int64_t start, int64_t B, int64_t L, int64_t H, int64_t D,
+    float eps, int interleaved, void* stream) {
+  return rope_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, io_dtype,
+                    q_weight, k_weight, weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype,
+                    q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity, start, B, L, H,
+                    D, eps, interleaved, stream, true);
+}

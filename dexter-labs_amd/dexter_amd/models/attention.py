@@ -1,0 +1,67 @@
+"""A self-attention layer that calls the path the way DreamZero's DiT does.
+
+Follows ``SelfAttention.forward`` (``models/dreamzero/model.py:158-183``):
+project q/k/v, QK-RMSNorm + rotary through ``ops.qk_norm_rope``, read
+``cache_len`` **before** appending, append k/v only when ``write``, attend
+with ``ops.blockwise_causal_attention`` over the cache plus the new block,
+project out. It exists to show the drop-in: nothing here names a kernel, the
+registry picks the gfx950 implementations.
+
+With ``write=True`` the prologue and the append run as one kernel
+(``KVCache.append_fused``). The projections are plain ``torch.nn.functional
+.linear`` (hipBLASLt); they are the caller's, not this path's.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .. import ops
+from .kv_cache import KVCache
+
+
+class SelfAttention(nn.Module):
+    def __init__(self, dim: int, heads: int, eps: float = 1e-6,
+                 dtype: torch.dtype = torch.bfloat16, device=None) -> None:
+        super().__init__()
+        if dim % heads:
+            raise ValueError("dim must be a multiple of heads")
+        self.heads, self.head_dim, self.eps = heads, dim // heads, eps
+        kw = dict(dtype=dtype, device=device)
+        self.q = nn.Linear(dim, dim, **kw)
+        self.k = nn.Linear(dim, dim, **kw)
+        self.v = nn.Linear(dim, dim, **kw)
+        self.o = nn.Linear(dim, dim, **kw)
+        # Wan's QK norm spans the full dim (applied before the head split).
+        self.q_norm = nn.Parameter(torch.ones(dim, **kw))
+        self.k_norm = nn.Parameter(torch.ones(dim, **kw))
+
+    @torch.no_grad()
+    def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                kv_cache: KVCache | None, layer: int,
+                block_boundaries: torch.Tensor | None = None, write: bool = False,
+                fused_append: bool = True) -> torch.Tensor:
+        b, seq, _ = x.shape
+        shape = (b, seq, self.heads, self.head_dim)
+        q = F.linear(x, self.q.weight, self.q.bias).view(shape)
+        k = F.linear(x, self.k.weight, self.k.bias).view(shape)
+        v = F.linear(x, self.v.weight, self.v.bias).view(shape)
+
+        cache_len = kv_cache.length if kv_cache is not None else 0
+        if kv_cache is not None and write and fused_append:
+            q, k = kv_cache.append_fused(layer, q, k, v, self.q_norm, self.k_norm, cos, sin,
+                                         self.eps)
+        else:
+            q, k = ops.qk_norm_rope(q, k, self.q_norm, self.k_norm, cos, sin, self.eps)
+            if kv_cache is not None and write:
+                kv_cache.append(layer, k, v)
+
+        out = ops.blockwise_causal_attention(
+            q, k, v,
+            kv_cache=kv_cache.cache[layer] if kv_cache is not None else None,
+            cache_len=cache_len,
+            block_boundaries=block_boundaries,
+        )
+        return F.linear(out.reshape(b, seq, -1), self.o.weight, self.o.bias)

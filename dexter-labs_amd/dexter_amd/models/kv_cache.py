@@ -1,0 +1,60 @@
+"""Per-layer self-attention KV cache (contract of ``models/dreamzero/model.py:35-65``).
+
+One ``[2, B, capacity, H, D]`` tensor per layer, allocated once for the
+episode. ``append(layer, k, v)`` writes rows ``[length, length+n)`` of both
+planes and does **not** move the cursor; ``commit(n)`` moves it once every
+layer has appended its block; ``reset()`` rewinds it. Overflow raises
+``RuntimeError("KV cache full: ...")`` before anything is written.
+
+Here ``append`` launches the HIP ``cache/append`` kernel through the op
+registry instead of two torch slice copies. ``append_fused`` is the
+``rope/qk_norm_rope_append`` form: the caller's prologue writes k and v into
+the slot in the same pass that produces q and k.
+
+Sizing on MI355X: a Wan-5B layer at 1,328 rows is 2 x 1328 x 24 x 128 x 2 B
+= 16.3 MB, so all 30 layers of a long episode fit many times over in 288 GB.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+
+
+class KVCache:
+    def __init__(self, layers: int, batch: int, capacity: int, heads: int, head_dim: int,
+                 device: torch.device | str, dtype: torch.dtype) -> None:
+        self.cache = [
+            torch.zeros(2, batch, capacity, heads, head_dim, device=device, dtype=dtype)
+            for _ in range(layers)
+        ]
+        self.capacity = capacity
+        self.length = 0
+
+    def _check_room(self, n: int) -> None:
+        if self.length + n > self.capacity:
+            raise RuntimeError(f"KV cache full: {self.length} + {n} > {self.capacity}")
+
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Write one block's k/v for ``layer`` at the cursor (cursor unchanged)."""
+        self._check_room(k.shape[1])
+        ops.kv_cache_append(self.cache[layer], k, v, self.length)
+
+    def append_fused(self, layer: int, q, k, v, q_weight, k_weight, cos, sin, eps=1e-6,
+                     interleaved=True):
+        """QK-norm + rotary on q/k, writing rotated k and raw v at the cursor.
+
+        Returns the rotated ``(q, k)``; equivalent to ``ops.qk_norm_rope``
+        followed by :meth:`append` of the rotated k.
+        """
+        self._check_room(k.shape[1])
+        return ops.qk_norm_rope_append(q, k, v, q_weight, k_weight, cos, sin,
+                                       self.cache[layer], self.length, eps, interleaved)
+
+    def commit(self, n: int) -> None:
+        """Advance the write cursor once every layer has appended its block."""
+        self.length += n
+
+    def reset(self) -> None:
+        self.length = 0

@@ -1,0 +1,126 @@
+"""Public op surface for the blockwise-causal attention path.
+
+Each function asks the registry for the best implementation on this platform
+and calls it, exactly as dexter's dispatchers do (``python/dexter/ops/__init__.py``):
+
+* ``qk_norm_rope``               -> ``select("rope", "qk_norm_rope", q, k)``
+  (reference ``ops/__init__.py:66-86``; same arguments and defaults)
+* ``blockwise_causal_attention`` -> ``select("attention", "blockwise_causal", q, k, v)``
+  (reference ``ops/__init__.py:127-147``; same keyword-only arguments)
+* ``kv_cache_append``            -> ``select("cache", "append", cache, k, v)``
+  (no dispatcher in the reference: ``KVCache.append`` does two torch slice
+  copies, ``models/dreamzero/model.py:53-58``; here it is a kernel too)
+
+Importing this module registers the gfx950 HIP kernels. Nothing else is
+registered, so on a machine without an MI355X every call raises
+``LookupError`` rather than running a slower stand-in.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ..registry import select
+
+__all__ = ["qk_norm_rope", "blockwise_causal_attention", "kv_cache_append",
+           "qk_norm_rope_append", "blockwise_causal_attention_varlen"]
+
+
+def qk_norm_rope(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float = 1e-6,
+    interleaved: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm over the whole ``H*D`` plane of each token, then rotary, for q and k.
+
+    ``q``/``k`` are ``[B, L, H, D]``; the weights are ``[H*D]``; ``cos``/``sin``
+    are ``[L, D//2]``. ``interleaved`` pairs ``(2j, 2j+1)`` (Wan); otherwise
+    ``(j, j + D/2)``. Returns new ``(q, k)`` tensors of the input dtype.
+    """
+    return select("rope", "qk_norm_rope", q, k)(
+        q, k, q_weight, k_weight, cos, sin, eps, interleaved)
+
+
+def blockwise_causal_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    kv_cache: torch.Tensor | None = None,
+    cache_len: int = 0,
+    block_boundaries: torch.Tensor | None = None,
+    softmax_scale: float | None = None,
+    causal: bool = False,
+) -> torch.Tensor:
+    """Softmax attention of ``q`` over ``[cache[:cache_len] | k]`` with block causality.
+
+    A query in the block starting at ``block_boundaries[i]`` sees the whole
+    cached history and every current key before the end of its own block.
+    ``None`` is one block (all current keys visible); ``causal=True`` is
+    token-causal on the current keys. ``kv_cache`` is ``[2, B, S, H, D]``;
+    rows ``[0, cache_len)`` are read in place, never copied.
+    """
+    return select("attention", "blockwise_causal", q, k, v)(
+        q, k, v, kv_cache, cache_len, block_boundaries, softmax_scale, causal)
+
+
+def blockwise_causal_attention_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    kv_cache: torch.Tensor,
+    cache_lens: list[int],
+    block_boundaries: torch.Tensor | None = None,
+    softmax_scale: float | None = None,
+    causal: bool = False,
+) -> torch.Tensor:
+    """``blockwise_causal_attention`` over a ragged batch in one launch.
+
+    Sequence ``b`` attends to ``kv_cache[:, b, :cache_lens[b]]`` followed by
+    its own ``k``/``v`` rows; results equal one ``blockwise_causal_attention``
+    call per sequence with ``cache_len=cache_lens[b]``. (The reference takes a
+    scalar ``cache_len`` only, so a ragged batch there is a loop of calls.)
+    """
+    return select("attention", "blockwise_causal_varlen", q, k, v)(
+        q, k, v, kv_cache, cache_lens, block_boundaries, softmax_scale, causal)
+
+
+def kv_cache_append(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    start: int) -> None:
+    """Write ``k``/``v`` ``[B, n, H, D]`` into rows ``[start, start+n)`` of both planes
+    of ``cache`` ``[2, B, S, H, D]``. Raises ``RuntimeError("KV cache full ...")``
+    when ``start + n > S``, before anything is launched.
+    """
+    return select("cache", "append", cache, k, v)(cache, k, v, start)
+
+
+def qk_norm_rope_append(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    cache: torch.Tensor,
+    start: int,
+    eps: float = 1e-6,
+    interleaved: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``qk_norm_rope`` and ``kv_cache_append`` of the rotated k and raw v, in one pass.
+
+    Same results as ``q, k = qk_norm_rope(...)`` followed by
+    ``kv_cache_append(cache, k, v, start)``.
+    """
+    return select("rope", "qk_norm_rope_append", q, k, v, cache)(
+        q, k, v, q_weight, k_weight, cos, sin, cache, start, eps, interleaved)
+
+
+# Importing the implementation package is what populates the registry.
+from . import gfx950  # noqa: E402,F401

@@ -1,0 +1,141 @@
+"""ctypes binding of libdexter_gfx950.so (declarations: include/dexter_gfx950.h).
+
+The library is loaded once per process, behind a lock, from the package
+directory where ``csrc/build.py`` puts it. There is no fallback: if the
+library is missing or was built for another ABI revision, loading raises, and
+so does every op that needs it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_NAME = "libdexter_gfx950.so"
+LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
+ABI_VERSION = 1
+
+DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
+DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
+
+_DTYPE_CODE = {torch.bfloat16: DX_BF16, torch.float16: DX_F16, torch.float32: DX_F32,
+               torch.int32: DX_I32, torch.int64: DX_I64}
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_l = ctypes.c_int64
+_f = ctypes.c_float
+
+# Argument lists, in the header's order.
+_SIGNATURES: dict[str, tuple[type, list]] = {
+    "dx_last_error": (ctypes.c_char_p, []),
+    "dx_abi_version": (_i, []),
+    "dx_qk_norm_rope": (_i, [
+        _p, _l, _l, _l,            # q, strides
+        _p, _l, _l, _l,            # k, strides
+        _i,                        # io dtype
+        _p, _p, _i,                # q_weight, k_weight, weight dtype
+        _p, _l, _p, _l, _i,        # cos, cos_sl, sin, sin_sl, table dtype
+        _p, _p,                    # q_out, k_out
+        _l, _l, _l, _l,            # B, L, H, D
+        _f, _i, _p]),              # eps, interleaved, stream
+    "dx_qk_norm_rope_append": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,            # v, strides
+        _i,
+        _p, _p, _i,
+        _p, _l, _p, _l, _i,
+        _p, _p,
+        _p, _l, _l, _l, _l, _l, _l,  # cache, plane, sb, ss, sh, capacity, start
+        _l, _l, _l, _l,
+        _f, _i, _p]),
+    "dx_kv_append": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l, _l,        # cache, plane, sb, ss, sh
+        _i, _l, _l, _l, _l,        # dtype, B, n, H, D
+        _l, _l, _p]),              # capacity, start, stream
+    "dx_blockwise_causal_attention": (_i, [
+        _p, _l, _l, _l,            # q
+        _p, _l, _l, _l,            # k
+        _p, _l, _l, _l,            # v
+        _p, _l, _l, _l, _l,        # cache, plane, sb, ss, sh
+        _p, _l, _l, _l,            # out
+        _i, _l, _l, _l, _l, _l,    # dtype, B, Lq, Lk, H, D
+        _l, _p, _i, _l,            # cache_len, starts, starts dtype, n_blocks
+        _i, _f,                    # causal, scale
+        _p, _l, _p]),              # workspace, bytes, stream
+    "dx_blockwise_causal_attention_varlen": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l, _l,
+        _p, _l, _l, _l,
+        _i, _l, _l, _l, _l, _l,
+        ctypes.POINTER(ctypes.c_int64), _p, _i, _l,
+        _i, _f,
+        _p, _l, _p]),
+    "dx_attention_workspace_bytes": (_l, [_l, _l, _l, _l, _l, _l]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def exported_symbols() -> list[str]:
+    """Every function name the header declares (and the loader binds)."""
+    return list(_SIGNATURES)
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library, with argument/return types set. Raises if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_NAME} is not built ({LIB_PATH}); run "
+                    "`python dexter-labs_amd/csrc/build.py` (or __graft_entry__.build())")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            got = lib.dx_abi_version()
+            if got != ABI_VERSION:
+                raise RuntimeError(f"{LIB_NAME} ABI {got}, expected {ABI_VERSION}; rebuild it")
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Turn a DX_E* return code into the matching Python exception."""
+    if rc == DX_OK:
+        return
+    msg = load().dx_last_error().decode(errors="replace")
+    if rc == DX_EFULL:
+        raise RuntimeError(msg)  # "KV cache full: ..." as the reference raises
+    if rc == DX_EINVAL:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (code {rc})")
+
+
+def dtype_code(t: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[t]
+    except KeyError:
+        raise ValueError(f"dtype {t} has no kernel") from None
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

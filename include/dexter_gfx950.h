@@ -1,0 +1,178 @@
+/*
+ * dexter_gfx950.h -- C ABI of the MI355X (gfx950) blockwise-causal attention path.
+ *
+ * One shared library, libdexter_gfx950.so, exports these entry points. They
+ * replace the device side of three pieces of dexter (raikonenfnu/dexter-labs),
+ * cited below as path:line under python/dexter/:
+ *
+ *   dx_qk_norm_rope          ops/gfx1151/rope/qk_norm_rope.py:93-110
+ *                            (semantics: ops/reference/rope.py:10-56,
+ *                             dispatcher ops/__init__.py:66-86)
+ *   dx_qk_norm_rope_append   the same, plus KVCache.append of the rotated k and
+ *                            the raw v (models/dreamzero/model.py:53-58,166-175)
+ *   dx_kv_append             KVCache.append, models/dreamzero/model.py:53-58
+ *   dx_blockwise_causal_attention
+ *                            ops/gfx1151/attention/blockwise_causal.py:146-173
+ *                            (semantics: ops/reference/attention.py:22-77,
+ *                             dispatcher ops/__init__.py:127-147)
+ *   dx_blockwise_causal_attention_varlen
+ *                            the same with one cache length per sequence; the
+ *                            reference has a scalar cache_len only, and a
+ *                            ragged batch there is one call per sequence.
+ *
+ * Conventions
+ *  - Tensors are device pointers with explicit element strides; the last
+ *    (head_dim) dimension must be contiguous. [B, L, H, D] tensors take
+ *    strides (sb, sl, sh). A KV cache [2, B, S, H, D] takes (plane, sb, ss, sh):
+ *    plane 0 holds K, plane 1 holds V.
+ *  - dtype codes: DX_BF16, DX_F16, DX_F32.
+ *  - stream is a hipStream_t (NULL = the legacy default stream). Every entry
+ *    point only enqueues work: no allocation, no host synchronisation, so the
+ *    calls are safe under HIP graph capture. Functions are re-entrant and may
+ *    be called from any host thread.
+ *  - Return 0 on success or a DX_E* code; dx_last_error() then describes the
+ *    failure of the calling thread's last failed call.
+ */
+#ifndef DEXTER_GFX950_H
+#define DEXTER_GFX950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DX_OK 0
+#define DX_EINVAL 1   /* bad shape, stride, dtype or argument */
+#define DX_ELAUNCH 2  /* the HIP runtime refused a launch */
+#define DX_EFULL 3    /* KV cache overflow: start + n > capacity */
+#define DX_EWORKSPACE 4 /* workspace smaller than dx_attention_workspace_bytes() */
+
+#define DX_BF16 0
+#define DX_F16 1
+#define DX_F32 2
+#define DX_I32 3
+#define DX_I64 4
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* dx_last_error(void);
+
+/* ABI revision of this header; the Python loader checks it. */
+int dx_abi_version(void);
+#define DX_ABI_VERSION 1
+
+/*
+ * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.
+ *   out = rope(round_io(x * rsqrt(mean(x^2 over H*D) + eps) * w))
+ * with the rotation in fp32 and a final round to the io dtype, the order of
+ * ops/reference/rope.py:29-40 then :10-26. interleaved != 0 pairs (2j, 2j+1);
+ * otherwise (j, j + D/2). cos/sin are [L, D/2] rows (row strides cos_sl,
+ * sin_sl), shared by every batch and head. q_out/k_out are contiguous
+ * [B, L, H, D]. io_dtype: DX_BF16 or DX_F16; weight_dtype and table_dtype:
+ * DX_BF16, DX_F16 or DX_F32.
+ * Replaces: ops/gfx1151/rope/qk_norm_rope.py:93-110.
+ */
+int dx_qk_norm_rope(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                    const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                    int io_dtype,
+                    const void* q_weight, const void* k_weight, int weight_dtype,
+                    const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl,
+                    int table_dtype,
+                    void* q_out, void* k_out,
+                    int64_t B, int64_t L, int64_t H, int64_t D,
+                    float eps, int interleaved, void* stream);
+
+/*
+ * dx_qk_norm_rope, and in the same pass the rotated k and the unmodified v
+ * [B, L, H, D] are written to rows [start, start + L) of the cache planes.
+ * Returns DX_EFULL (nothing launched) when start + L > capacity.
+ * Replaces: ops/gfx1151/rope/qk_norm_rope.py:93-110 followed by
+ * models/dreamzero/model.py:53-58 (KVCache.append).
+ */
+int dx_qk_norm_rope_append(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                           const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                           const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+                           int io_dtype,
+                           const void* q_weight, const void* k_weight, int weight_dtype,
+                           const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl,
+                           int table_dtype,
+                           void* q_out, void* k_out,
+                           void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
+                           int64_t c_sh, int64_t capacity, int64_t start,
+                           int64_t B, int64_t L, int64_t H, int64_t D,
+                           float eps, int interleaved, void* stream);
+
+/*
+ * Copy k and v [B, n, H, D] into rows [start, start + n) of planes 0 and 1 of
+ * a [2, B, capacity, H, D] cache. Bit-exact copy. dtype: DX_BF16, DX_F16 or
+ * DX_F32. Returns DX_EFULL (nothing launched) when start + n > capacity.
+ * Replaces: models/dreamzero/model.py:53-58 (KVCache.append).
+ */
+int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                 const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+                 void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                 int dtype, int64_t B, int64_t n, int64_t H, int64_t D,
+                 int64_t capacity, int64_t start, void* stream);
+
+/*
+ * Blockwise-causal flash attention forward.
+ *   keys/values = [cache rows 0..cache_len) | k/v rows 0..Lk)]
+ *   query i sees key j iff j < cache_len + end(i), where end(i) is
+ *     causal != 0          : i + 1
+ *     n_blocks == 0        : Lk (one block: every current key)
+ *     otherwise            : the largest block end among blocks [s_b, s_{b+1})
+ *                            (last end = Lq) containing i; 0 if none does
+ *   (ops/reference/attention.py:22-47). Lk must equal Lq, as the reference's
+ *   mask shape requires. A query with no visible key yields NaN, as the
+ *   reference's softmax over an all -inf row does.
+ * block_starts: device pointer to n_blocks int32 (starts_dtype DX_I32) or
+ * int64 (DX_I64) block start indices, read on the device (no host sync).
+ * softmax_scale multiplies q.k before the softmax (the reference's default
+ * is 1/sqrt(D); callers pass it explicitly). dtype: DX_BF16 or DX_F16;
+ * D: 64 or 128.
+ * out may be strided like q. cache may be NULL when cache_len == 0.
+ * workspace must hold dx_attention_workspace_bytes(...) bytes for the same
+ * shape (it may be NULL when that is 0); its contents need no initialisation.
+ * Replaces: ops/gfx1151/attention/blockwise_causal.py:146-173.
+ */
+int dx_blockwise_causal_attention(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+    const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+    void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D,
+    int64_t cache_len, const void* block_starts, int starts_dtype, int64_t n_blocks,
+    int causal, float softmax_scale,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * As dx_blockwise_causal_attention, with cache_lens[b] (a host array of B
+ * values, copied into the launch arguments) as sequence b's cached length.
+ * B <= 64.
+ */
+int dx_blockwise_causal_attention_varlen(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+    const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+    void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D,
+    const int64_t* cache_lens, const void* block_starts, int starts_dtype,
+    int64_t n_blocks, int causal, float softmax_scale,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes the attention entry points need for this shape on the
+ * current device (split-KV partial results); 0 when the launch does not split.
+ * max_cache_len is cache_len, or the largest cache_lens[b] for varlen.
+ * Returns a negative DX_E* code on a bad shape.
+ */
+int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
+                                     int64_t D, int64_t max_cache_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DEXTER_GFX950_H */

@@ -1,0 +1,94 @@
+"""fp64 brute force of the path, independent of the torch restatements.
+
+Written from the definitions, not from the torch code: attention is an
+explicit loop over (batch, head, query) with a stable softmax over exactly
+the visible keys (decided per key by the rule of
+``ops/reference/attention.py:22-47``); the prologue is numpy float64 with no
+intermediate rounding (the reference's bf16 rounding after the norm,
+``ops/reference/rope.py:40``, is applied only when ``round_to`` is given).
+Meant for small inputs (config C0 and the like): it is slow on purpose.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def key_visible(i: int, j: int, q_len: int, cache_len: int, starts, causal: bool) -> bool:
+    """Whether query ``i`` may attend to key ``j`` (key 0 = first cached row)."""
+    if j < cache_len:
+        return True
+    jj = j - cache_len
+    if causal:
+        return jj <= i
+    if starts is None:
+        return True
+    bounds = list(starts) + [q_len]
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        if lo <= i < hi and jj < hi:
+            return True
+    return False
+
+
+def attention(q, k, v, cache_k=None, cache_v=None, cache_len=0, starts=None,
+              causal=False, scale=None):
+    """q/k/v: arrays ``[B, L, H, D]``; cache_k/v ``[B, S, H, D]``. Returns fp64 ``[B, L, H, D]``.
+
+    A query with no visible key gives NaN (0/0), as a softmax over nothing.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    b, q_len, h, d = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if cache_len > 0:
+        keys = np.concatenate([np.asarray(cache_k, np.float64)[:, :cache_len], k], axis=1)
+        vals = np.concatenate([np.asarray(cache_v, np.float64)[:, :cache_len], v], axis=1)
+    else:
+        keys, vals = k, v
+    n_keys = keys.shape[1]
+    out = np.empty((b, q_len, h, d), dtype=np.float64)
+    for i in range(q_len):
+        vis = np.array([key_visible(i, j, q_len, cache_len, starts, causal) for j in range(n_keys)])
+        for bb in range(b):
+            for hh in range(h):
+                if not vis.any():
+                    out[bb, i, hh] = np.nan
+                    continue
+                s = keys[bb, vis, hh] @ q[bb, i, hh] * scale
+                w = np.exp(s - s.max())
+                out[bb, i, hh] = (w[:, None] * vals[bb, vis, hh]).sum(0) / w.sum()
+    return out
+
+
+def qk_norm_rope(x, weight, cos, sin, eps=1e-6, interleaved=True, round_to=None):
+    """One tensor ``[B, L, H, D]`` through plane-RMSNorm then rotary, in fp64.
+
+    ``round_to`` (a callable float64 -> float64) models the reference's cast
+    to the input dtype between norm and rotation.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    b, seq, h, d = x.shape
+    plane = x.reshape(b, seq, h * d)
+    rms = np.sqrt((plane ** 2).mean(-1, keepdims=True) + eps)
+    y = (plane / rms * np.asarray(weight, np.float64).reshape(1, 1, -1)).reshape(b, seq, h, d)
+    if round_to is not None:
+        y = round_to(y)
+    c = np.asarray(cos, np.float64)[None, :, None, :]
+    s = np.asarray(sin, np.float64)[None, :, None, :]
+    out = np.empty_like(y)
+    if interleaved:
+        lo, hi = y[..., 0::2], y[..., 1::2]
+        out[..., 0::2] = lo * c - hi * s
+        out[..., 1::2] = lo * s + hi * c
+    else:
+        half = d // 2
+        lo, hi = y[..., :half], y[..., half:]
+        out[..., :half] = lo * c - hi * s
+        out[..., half:] = lo * s + hi * c
+    return out

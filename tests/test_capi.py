@@ -1,0 +1,74 @@
+"""The C-ABI library: it loads and exports every symbol the header declares.
+
+No device work happens here: only calls that fail argument validation before
+touching the HIP runtime, and the version query.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from dexter_amd.ops.gfx950 import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dexter_gfx950.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for want in ("dx_qk_norm_rope", "dx_qk_norm_rope_append", "dx_kv_append",
+                 "dx_blockwise_causal_attention", "dx_blockwise_causal_attention_varlen",
+                 "dx_attention_workspace_bytes", "dx_last_error", "dx_abi_version"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol(built_lib):
+    lib = ctypes.CDLL(str(built_lib))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_loader_binds_exactly_the_header(built_lib):
+    assert sorted(_lib.exported_symbols()) == declared_functions()
+
+
+def test_abi_version(built_lib):
+    lib = _lib.load()
+    assert lib.dx_abi_version() == _lib.ABI_VERSION
+    header_version = int(re.search(r"#define DX_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert header_version == _lib.ABI_VERSION
+
+
+def test_overflow_is_reported_before_any_launch(built_lib):
+    lib = _lib.load()
+    rc = lib.dx_kv_append(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, 0,
+                          _lib.DX_BF16, 1, 5, 2, 64, 8, 4, None)
+    assert rc == _lib.DX_EFULL
+    assert lib.dx_last_error().decode() == "KV cache full: 4 + 5 > 8"
+    with pytest.raises(RuntimeError, match="KV cache full: 4 \\+ 5 > 8"):
+        _lib.check(rc, "kv_append")
+
+
+def test_bad_arguments_are_rejected(built_lib):
+    lib = _lib.load()
+    rc = lib.dx_kv_append(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, 0,
+                          99, 1, 1, 2, 64, 8, 0, None)
+    assert rc == _lib.DX_EINVAL and "dtype" in lib.dx_last_error().decode()
+    args = [16, 0, 0, 0] * 3 + [None, 0, 0, 0, 0] + [16, 0, 0, 0]
+    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 8, 2, 96, 0, None,
+                                           _lib.DX_I32, 0, 0, 1.0, None, 0, None)
+    assert rc == _lib.DX_EINVAL and "head_dim 96" in lib.dx_last_error().decode()
+    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 9, 2, 128, 0, None,
+                                           _lib.DX_I32, 0, 0, 1.0, None, 0, None)
+    assert rc == _lib.DX_EINVAL and "must equal q length" in lib.dx_last_error().decode()
+    with pytest.raises(ValueError, match="must equal q length"):
+        _lib.check(rc, "attention")

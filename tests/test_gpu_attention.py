@@ -1,0 +1,233 @@
+"""HIP blockwise-causal attention against the oracle (MI355X).
+
+The first three tests restate the reference suite's attention tests
+(``test/test_ops.py:93-103, 118-135, 166-181``) with the oracle in place of
+the REFERENCE spec; the rest widen coverage: both MFMA dtypes and head dims,
+ragged tile edges, split-KV, strided inputs, fully masked rows, bit-exact
+future invisibility, and the ragged-batch entry point.
+
+Parity bar (bf16/f16 kernel vs fp32 oracle on identical inputs): max-abs
+<= 2e-2, mean-abs <= 2e-3; the reference's own relative check (3e-2) too.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import dexter_amd.ops as ops
+from dexter_amd.registry import select_spec
+from oracle import attention as oatt
+
+from _util import assert_parity, close_rel
+
+pytestmark = pytest.mark.gpu
+DT = torch.bfloat16
+
+
+def _oracle(q, k, v, cache, cache_len, bb, scale=None, causal=False):
+    return oatt.blockwise_causal_attention(
+        q.cpu(), k.cpu(), v.cpu(), None if cache is None else cache.cpu(), cache_len,
+        None if bb is None else bb.cpu(), scale, causal, keep_fp32=True)
+
+
+def _rand(shape, device, dtype=DT, scale=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype).to(device)
+
+
+def test_selected_kernel_is_hip(device, built_lib):
+    q = torch.zeros(1, 8, 2, 128, dtype=DT, device=device)
+    assert select_spec("attention", "blockwise_causal", q, q, q).name == "hip_blockwise_causal_gfx950"
+
+
+@pytest.mark.parametrize("cache_len", [0, 256])
+@pytest.mark.parametrize("blocks", [None, [0, 50, 100]])
+def test_attention(device, built_lib, cache_len, blocks):
+    b, l, h, d = 1, 125, 24, 128
+    q = _rand((b, l, h, d), device, scale=0.3, seed=1)
+    k = _rand((b, l, h, d), device, seed=2)
+    v = _rand((b, l, h, d), device, seed=3)
+    cache = _rand((2, b, 512, h, d), device, scale=0.3, seed=4) if cache_len else None
+    bb = torch.tensor(blocks, device=device) if blocks else None
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
+                                         block_boundaries=bb)
+    ref = _oracle(q, k, v, cache, cache_len, bb)
+    assert got.dtype == DT and got.shape == q.shape
+    assert_parity(got, ref, what=f"cache_len={cache_len} blocks={blocks}")
+    close_rel(got, ref, tol=3e-2)
+
+
+@pytest.mark.parametrize("scale", [1.0, 60.0])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_attention_survives_extreme_scores(device, built_lib, scale, sign):
+    b, l, h, d = 1, 96, 4, 128
+    q = torch.full((b, l, h, d), sign * scale, device=device, dtype=DT)
+    k = torch.full((b, l, h, d), scale, device=device, dtype=DT)
+    v = _rand((b, l, h, d), device, seed=5)
+    bb = torch.tensor([0, 48], device=device)
+    got = ops.blockwise_causal_attention(q, k, v, block_boundaries=bb)
+    assert torch.isfinite(got.float()).all(), "attention produced non-finite output"
+    ref = _oracle(q, k, v, None, 0, bb)
+    assert_parity(got, ref)
+    close_rel(got, ref, tol=3e-2)
+
+
+@pytest.mark.parametrize("cache_len", [0, 32])
+def test_attention_causal_matches_reference(device, built_lib, cache_len):
+    b, l, h, d = 1, 64, 4, 128
+    q = _rand((b, l, h, d), device, scale=0.3, seed=6)
+    k = _rand((b, l, h, d), device, scale=0.3, seed=7)
+    v = _rand((b, l, h, d), device, scale=0.3, seed=8)
+    cache = _rand((2, b, 128, h, d), device, scale=0.3, seed=9) if cache_len else None
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len, causal=True)
+    ref = _oracle(q, k, v, cache, cache_len, None, causal=True)
+    assert_parity(got, ref)
+    # A causal query must not see the future: bumping the last key changes only
+    # the last row -- bit-exactly here, not just within a tolerance.
+    k2 = k.clone()
+    k2[:, -1] += 5.0
+    other = ops.blockwise_causal_attention(q, k2, v, kv_cache=cache, cache_len=cache_len,
+                                           causal=True)
+    assert torch.equal(got[:, :-1], other[:, :-1])
+    assert not torch.equal(got[:, -1:], other[:, -1:])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("q_len,cache_len,blocks", [
+    (1, 0, None), (31, 0, [0, 7, 19]), (83, 1245, None), (99, 332, [0, 83]),
+    (130, 63, [0, 64, 65]), (200, 1, [0, 100]), (257, 0, None),
+])
+def test_shapes_and_dtypes(device, built_lib, dtype, d, q_len, cache_len, blocks):
+    b, h = 2, 3
+    q = _rand((b, q_len, h, d), device, dtype, seed=10)
+    k = _rand((b, q_len, h, d), device, dtype, seed=11)
+    v = _rand((b, q_len, h, d), device, dtype, seed=12)
+    cache = _rand((2, b, cache_len + 5, h, d), device, dtype, seed=13) if cache_len else None
+    bb = torch.tensor(blocks, device=device, dtype=torch.int64) if blocks else None
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
+                                         block_boundaries=bb)
+    ref = _oracle(q, k, v, cache, cache_len, bb)
+    assert got.dtype == dtype
+    assert_parity(got, ref, what=f"{dtype} d={d} q={q_len} cache={cache_len} blocks={blocks}")
+
+
+def test_explicit_scale_and_strided_inputs(device, built_lib):
+    b, l, h, d = 2, 70, 4, 128
+    base = _rand((b, h, l, d), device, seed=14)           # [B, H, L, D] storage
+    q = base.transpose(1, 2)                              # strided [B, L, H, D] view
+    k = _rand((b, l, h, d), device, seed=15)
+    v = _rand((b, l, 2 * h, d), device, seed=16)[:, :, ::2]  # head stride 2*D
+    got = ops.blockwise_causal_attention(q, k, v, softmax_scale=0.05,
+                                         block_boundaries=torch.tensor([0, 30], device=device))
+    ref = _oracle(q, k, v, None, 0, torch.tensor([0, 30]), scale=0.05)
+    assert_parity(got, ref)
+
+
+def test_split_kv_decode_shape(device, built_lib):
+    """The Wan-5B chunk shape: 83 queries over 1245 cached + 83 new keys (split-KV path)."""
+    b, l, h, d, cache_len = 1, 83, 24, 128, 1245
+    q = _rand((b, l, h, d), device, seed=17)
+    k = _rand((b, l, h, d), device, seed=18)
+    v = _rand((b, l, h, d), device, seed=19)
+    cache = _rand((2, b, 1328, h, d), device, seed=20)
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len)
+    ref = _oracle(q, k, v, cache, cache_len, None)
+    assert_parity(got, ref)
+
+
+def test_rows_before_the_first_block_match_the_reference(device, built_lib):
+    """Rows before block_boundaries[0] see only the cache; with no cache they are NaN."""
+    b, l, h, d = 1, 40, 2, 64
+    q, k, v = (_rand((b, l, h, d), device, seed=s) for s in (21, 22, 23))
+    bb = torch.tensor([8, 20], device=device)
+    got = ops.blockwise_causal_attention(q, k, v, block_boundaries=bb)
+    ref = _oracle(q, k, v, None, 0, bb)
+    assert torch.isnan(got[:, :8].float()).all() and torch.isnan(ref[:, :8]).all()
+    assert_parity(got[:, 8:], ref[:, 8:])
+    cache = _rand((2, b, 16, h, d), device, seed=24)
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=16, block_boundaries=bb)
+    assert_parity(got, _oracle(q, k, v, cache, 16, bb))
+
+
+def test_empty_block_list_sees_only_history(device, built_lib):
+    b, l, h, d = 1, 16, 2, 64
+    q, k, v = (_rand((b, l, h, d), device, seed=s) for s in (25, 26, 27))
+    cache = _rand((2, b, 8, h, d), device, seed=28)
+    bb = torch.zeros(0, dtype=torch.int64, device=device)
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=8, block_boundaries=bb)
+    assert_parity(got, _oracle(q, k, v, cache, 8, bb))
+
+
+@pytest.mark.parametrize("poison", ["finite", "inf", "nan"])
+def test_future_blocks_are_invisible_bit_exact(device, built_lib, poison):
+    """Whatever the keys/values of a future block hold, earlier blocks' outputs do not move.
+
+    Blocks are 128 queries long (a whole query tile), so a future block's rows
+    are never even loaded by the workgroups of earlier blocks: NaN/Inf there
+    cannot leak through 0 * Inf.
+    """
+    b, l, h, d = 1, 384, 4, 128
+    q, k, v = (_rand((b, l, h, d), device, seed=s) for s in (29, 30, 31))
+    cache = _rand((2, b, 64, h, d), device, seed=32)
+    bb = torch.tensor([0, 128, 256], device=device)
+    base = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=64, block_boundaries=bb)
+    k2, v2 = k.clone(), v.clone()
+    fill = {"finite": 3.0, "inf": float("inf"), "nan": float("nan")}[poison]
+    k2[:, 256:] = fill
+    v2[:, 256:] = fill
+    other = ops.blockwise_causal_attention(q, k2, v2, kv_cache=cache, cache_len=64,
+                                           block_boundaries=bb)
+    assert torch.equal(base[:, :256], other[:, :256])
+    assert_parity(base, _oracle(q, k, v, cache, 64, bb))
+
+
+def test_future_block_perturbation_unaligned_blocks(device, built_lib):
+    """Blocks of 83 tokens (not tile aligned): finite changes to a future block stay invisible."""
+    b, l, h, d = 1, 249, 4, 128
+    q, k, v = (_rand((b, l, h, d), device, seed=s) for s in (33, 34, 35))
+    bb = torch.tensor([0, 83, 166], device=device)
+    base = ops.blockwise_causal_attention(q, k, v, block_boundaries=bb)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, 166:] *= -2.0
+    v2[:, 166:] += 1.5
+    other = ops.blockwise_causal_attention(q, k2, v2, block_boundaries=bb)
+    assert torch.equal(base[:, :166], other[:, :166])
+    assert not torch.equal(base[:, 166:], other[:, 166:])
+
+
+def test_varlen_matches_per_sequence_calls(device, built_lib):
+    h, d, q_len = 4, 128, 99
+    lens = [0, 40, 300, 131]
+    b = len(lens)
+    q = _rand((b, q_len, h, d), device, seed=36)
+    k = _rand((b, q_len, h, d), device, seed=37)
+    v = _rand((b, q_len, h, d), device, seed=38)
+    cache = _rand((2, b, max(lens), h, d), device, seed=39)
+    bb = torch.tensor([0, 83], device=device)
+    got = ops.blockwise_causal_attention_varlen(q, k, v, kv_cache=cache, cache_lens=lens,
+                                                block_boundaries=bb)
+    for i, c in enumerate(lens):
+        ref = _oracle(q[i:i + 1], k[i:i + 1], v[i:i + 1], cache[:, i:i + 1], c, bb)
+        assert_parity(got[i:i + 1], ref, what=f"seq {i} cache {c}")
+        one = ops.blockwise_causal_attention(q[i:i + 1], k[i:i + 1], v[i:i + 1],
+                                             kv_cache=cache[:, i:i + 1].contiguous() if c else None,
+                                             cache_len=c, block_boundaries=bb)
+        assert_parity(one, ref)
+
+
+def test_kv_length_mismatch_is_an_error(device, built_lib):
+    q = torch.zeros(1, 8, 2, 64, dtype=DT, device=device)
+    k = torch.zeros(1, 9, 2, 64, dtype=DT, device=device)
+    with pytest.raises(ValueError, match="must equal q length"):
+        ops.blockwise_causal_attention(q, k, k)
+
+
+def test_default_scale(device, built_lib):
+    q, k, v = (_rand((1, 40, 2, 64), device, seed=s) for s in (40, 41, 42))
+    a = ops.blockwise_causal_attention(q, k, v)
+    b = ops.blockwise_causal_attention(q, k, v, softmax_scale=1.0 / math.sqrt(64))
+    assert torch.equal(a, b)

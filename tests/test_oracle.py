@@ -1,0 +1,309 @@
+"""Pin the CPU oracle before trusting it (no GPU).
+
+The reference ships no golden vectors for this path, so each oracle function
+is pinned three independent ways, chosen so that a plausible mistake (a
+dropped scale, a mask off by one block, a transposed operand, a lost
+rounding step) fails at least one:
+
+* an fp64 brute force written from the definitions (``oracle/brute.py``);
+* a library routine: ``torch.nn.functional.scaled_dot_product_attention``;
+* closed forms: identical keys average exactly the visible values; one-hot
+  values read out the attention probabilities; RoPE preserves pair norms;
+  ``cos=1, sin=0`` reduces to the plain RMS norm.
+
+The last tests plant mistakes in copies of the oracle and check the pins
+catch them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as oatt
+from oracle import brute
+from oracle import kv_cache as okv
+from oracle import rope as orope
+
+
+def _c0_inputs():
+    from dexter_amd.bench.workloads import CONFIGS, make_inputs
+    return make_inputs(CONFIGS["C0"])
+
+
+# ---------------------------------------------------------------- mask -----
+
+@pytest.mark.parametrize("cache_len", [0, 5])
+@pytest.mark.parametrize("mode", ["none", "causal", "blocks", "ragged_blocks", "late_first"])
+def test_mask_matches_brute_rule(cache_len, mode):
+    q_len = 13
+    starts = {"none": None, "causal": None, "blocks": [0, 4, 9],
+              "ragged_blocks": [0, 1, 7, 12], "late_first": [3, 8]}[mode]
+    causal = mode == "causal"
+    bb = torch.tensor(starts) if starts is not None else None
+    mask = oatt.block_causal_mask(q_len, cache_len, bb, causal=causal)
+    assert mask.shape == (q_len, cache_len + q_len)
+    for i in range(q_len):
+        for j in range(cache_len + q_len):
+            assert bool(mask[i, j]) == brute.key_visible(i, j, q_len, cache_len, starts, causal)
+
+
+def test_mask_c0_structure():
+    """C0: 3 blocks of 16; block b sees keys [0, 16(b+1)) exactly."""
+    mask = oatt.block_causal_mask(48, 0, torch.tensor([0, 16, 32]))
+    for b in range(3):
+        rows = mask[16 * b:16 * (b + 1)]
+        assert rows[:, :16 * (b + 1)].all()
+        assert not rows[:, 16 * (b + 1):].any()
+
+
+# ----------------------------------------------------------- attention -----
+
+def test_c0_matches_fp64_brute_force():
+    inp = _c0_inputs()
+    q, k, v = inp.q, inp.k, inp.v
+    got = oatt.blockwise_causal_attention(q, k, v, None, 0, torch.tensor([0, 16, 32]), None)
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy(), starts=[0, 16, 32])
+    assert got.dtype == torch.float32
+    np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("cache_len", [0, 7])
+@pytest.mark.parametrize("causal", [False, True])
+def test_with_cache_matches_fp64_brute_force(cache_len, causal):
+    g = torch.Generator().manual_seed(11)
+    b, l, h, d, s = 2, 10, 3, 16, 12
+    q, k, v = (torch.randn(b, l, h, d, generator=g) for _ in range(3))
+    cache = torch.randn(2, b, s, h, d, generator=g)
+    starts = None if causal else [0, 3, 8]
+    bb = None if starts is None else torch.tensor(starts)
+    got = oatt.blockwise_causal_attention(q, k, v, cache, cache_len, bb, 0.37, causal)
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy(), cache[0].numpy(), cache[1].numpy(),
+                          cache_len, starts, causal, scale=0.37)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("mode", ["blocks", "causal", "none"])
+def test_matches_sdpa(mode):
+    g = torch.Generator().manual_seed(3)
+    b, l, h, d, cache_len = 1, 40, 4, 64, 24
+    q, k, v = (torch.randn(b, l, h, d, generator=g) for _ in range(3))
+    cache = torch.randn(2, b, 32, h, d, generator=g)
+    bb = torch.tensor([0, 10, 25]) if mode == "blocks" else None
+    got = oatt.blockwise_causal_attention(q, k, v, cache, cache_len, bb, None, mode == "causal")
+    keys = torch.cat((cache[0, :, :cache_len], k), 1).transpose(1, 2)
+    vals = torch.cat((cache[1, :, :cache_len], v), 1).transpose(1, 2)
+    mask = oatt.block_causal_mask(l, cache_len, bb, causal=mode == "causal")
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), keys, vals, attn_mask=mask)
+    torch.testing.assert_close(got, ref.transpose(1, 2), rtol=0, atol=2e-6)
+
+
+def test_no_mask_is_plain_softmax_attention():
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(1, 20, 2, 32, generator=g) for _ in range(3))
+    got = oatt.blockwise_causal_attention(q, k, v)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    torch.testing.assert_close(got, ref.transpose(1, 2), rtol=0, atol=2e-6)
+
+
+def test_identical_keys_average_exactly_the_visible_values():
+    """All keys equal => uniform weights over the visible set: the mean of visible v rows."""
+    g = torch.Generator().manual_seed(8)
+    b, l, h, d, cache_len = 1, 12, 2, 8, 4
+    q = torch.randn(b, l, h, d, generator=g)
+    k = torch.ones(b, l, h, d)
+    v = torch.randn(b, l, h, d, generator=g, dtype=torch.float64).float()
+    cache = torch.zeros(2, b, 6, h, d)
+    cache[0, :, :cache_len] = 1.0
+    cache[1, :, :cache_len] = torch.randn(b, cache_len, h, d, generator=g)
+    starts = [0, 5, 9]
+    got = oatt.blockwise_causal_attention(q, k, v, cache, cache_len, torch.tensor(starts), None)
+    vals = torch.cat((cache[1, :, :cache_len], v), 1)
+    ends = [5] * 5 + [9] * 4 + [12] * 3
+    for i in range(l):
+        expect = vals[:, : cache_len + ends[i]].mean(1)
+        torch.testing.assert_close(got[:, i], expect, rtol=0, atol=1e-6)
+
+
+def test_one_hot_values_read_out_probabilities():
+    """v[j] = e_j => out[i, j] = P(i attends j); future-block probabilities are exactly 0."""
+    g = torch.Generator().manual_seed(9)
+    l, d = 48, 64
+    q = torch.randn(1, l, 1, d, generator=g)
+    k = torch.randn(1, l, 1, d, generator=g)
+    v = torch.zeros(1, l, 1, d)
+    v[0, torch.arange(l), 0, torch.arange(l)] = 1.0
+    p = oatt.blockwise_causal_attention(q, k, v, None, 0, torch.tensor([0, 16, 32]), None)[0, :, 0, :l]
+    for blk in range(3):
+        rows = p[16 * blk:16 * (blk + 1)]
+        assert torch.equal(rows[:, 16 * (blk + 1):], torch.zeros_like(rows[:, 16 * (blk + 1):]))
+        torch.testing.assert_close(rows.sum(1), torch.ones(16), rtol=0, atol=1e-6)
+
+
+def test_future_blocks_are_invisible_bit_exact():
+    inp = _c0_inputs()
+    q, k, v = inp.q, inp.k, inp.v
+    bb = torch.tensor([0, 16, 32])
+    base = oatt.blockwise_causal_attention(q, k, v, None, 0, bb, None)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, 32:] += 7.0
+    v2[:, 32:] = -v2[:, 32:] * 3.0
+    other = oatt.blockwise_causal_attention(q, k2, v2, None, 0, bb, None)
+    assert torch.equal(base[:, :32], other[:, :32])
+    assert not torch.equal(base[:, 32:], other[:, 32:])
+
+
+def test_rows_before_first_block_are_nan_without_cache():
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(1, 12, 2, 16, generator=g) for _ in range(3))
+    out = oatt.blockwise_causal_attention(q, k, v, None, 0, torch.tensor([4, 8]), None)
+    assert torch.isnan(out[:, :4]).all()
+    assert torch.isfinite(out[:, 4:]).all()
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy(), starts=[4, 8])
+    assert np.isnan(ref[:, :4]).all()
+
+
+def test_output_dtype_follows_q():
+    q = torch.randn(1, 8, 2, 16).bfloat16()
+    out = oatt.blockwise_causal_attention(q, q, q)
+    assert out.dtype == torch.bfloat16
+    assert oatt.blockwise_causal_attention(q, q, q, keep_fp32=True).dtype == torch.float32
+
+
+# ---------------------------------------------------------------- rope -----
+
+def _bf16_round(x: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(x).to(torch.float32).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def _rope_inputs(seed=0, b=1, l=6, h=3, d=16, dtype=torch.bfloat16):
+    from dexter_amd.bench.workloads import rope_table
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, l, h, d, generator=g).to(dtype)
+    k = torch.randn(b, l, h, d, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(h * d, generator=g)).to(dtype)
+    cos, sin = rope_table(torch.arange(l) + 3, d)
+    return q, k, w, cos, sin
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_rope_matches_fp64_with_the_reference_rounding(interleaved):
+    q, k, w, cos, sin = _rope_inputs()
+    got_q, _ = orope.qk_norm_rope(q, k, w, w, cos, sin, 1e-6, interleaved, keep_fp32=True)
+    ref = brute.qk_norm_rope(q.float().numpy(), w.float().numpy(), cos.numpy(), sin.numpy(),
+                             1e-6, interleaved, round_to=_bf16_round)
+    # fp32 arithmetic on bf16-rounded operands: agreement to a few fp32 ulps,
+    # except where the fp32 norm lands on the other side of a bf16 rounding tie.
+    diff = np.abs(got_q.numpy() - ref)
+    assert np.quantile(diff, 0.99) < 1e-5
+    assert diff.max() < 2e-2
+
+
+def test_rope_identity_rotation_is_plain_rms_norm():
+    q, k, w, cos, sin = _rope_inputs(l=4)
+    one, zero = torch.ones_like(cos), torch.zeros_like(sin)
+    got, _ = orope.qk_norm_rope(q, k, w, w, one, zero, 1e-6, True, keep_fp32=True)
+    plane = q.float().reshape(1, 4, -1)
+    expect = (plane / torch.sqrt(plane.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float())
+    expect = expect.to(torch.bfloat16).float().reshape(q.shape)
+    torch.testing.assert_close(got, expect, rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_rope_preserves_pair_norms(interleaved):
+    q, k, w, cos, sin = _rope_inputs(dtype=torch.float32)
+    normed = orope.rms_norm(q, w, 1e-6)
+    rot = orope.rotary(normed, cos, sin, interleaved)
+    if interleaved:
+        a = normed[..., 0::2] ** 2 + normed[..., 1::2] ** 2
+        b = rot[..., 0::2] ** 2 + rot[..., 1::2] ** 2
+    else:
+        h = q.shape[-1] // 2
+        a = normed[..., :h] ** 2 + normed[..., h:] ** 2
+        b = rot[..., :h] ** 2 + rot[..., h:] ** 2
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
+def test_unit_weight_gives_unit_plane_rms():
+    q, k, _, cos, sin = _rope_inputs(dtype=torch.float32, h=4, d=32)
+    w = torch.ones(4 * 32)
+    out, _ = orope.qk_norm_rope(q, k, w, w, cos, sin, 0.0, True)
+    rms = out.reshape(1, out.shape[1], -1).pow(2).mean(-1).sqrt()
+    torch.testing.assert_close(rms, torch.ones_like(rms), rtol=1e-5, atol=1e-5)
+
+
+def test_pairings_differ():
+    q, k, w, cos, sin = _rope_inputs()
+    a, _ = orope.qk_norm_rope(q, k, w, w, cos, sin, 1e-6, True)
+    b, _ = orope.qk_norm_rope(q, k, w, w, cos, sin, 1e-6, False)
+    assert not torch.allclose(a.float(), b.float(), atol=1e-3)
+
+
+# ------------------------------------------------------------ kv cache -----
+
+def test_kv_cache_contract():
+    c = okv.KVCache(layers=2, batch=1, capacity=10, heads=2, head_dim=8)
+    blocks = []
+    for step in range(2):
+        k = torch.randn(1, 4, 2, 8).bfloat16()
+        v = torch.randn(1, 4, 2, 8).bfloat16()
+        for layer in range(2):
+            c.append(layer, k, v)
+        assert c.length == 4 * step  # append does not move the cursor
+        c.commit(4)
+        blocks.append((k, v))
+    assert torch.equal(c.cache[1][0, :, :8], torch.cat([b[0] for b in blocks], 1))
+    assert torch.equal(c.cache[1][1, :, :8], torch.cat([b[1] for b in blocks], 1))
+    with pytest.raises(RuntimeError, match="KV cache full"):
+        c.append(0, torch.zeros(1, 4, 2, 8).bfloat16(), torch.zeros(1, 4, 2, 8).bfloat16())
+    c.reset()
+    assert c.length == 0
+
+
+# --------------------------------------------- the pins catch mistakes -----
+
+def _planted_scale_dropped(q, k, v, *a, **kw):
+    return oatt.blockwise_causal_attention(q, k, v, *a[:3], softmax_scale=1.0, **kw)
+
+
+def _planted_mask_one_block_late(q, k, v, kv_cache, cache_len, bb, scale):
+    shifted = None if bb is None else torch.cat((bb[:1], bb[2:]))
+    return oatt.blockwise_causal_attention(q, k, v, kv_cache, cache_len, shifted, scale)
+
+
+def _planted_kt_not_transposed(q, k, v, kv_cache, cache_len, bb, scale):
+    # Keys read with head and position swapped: a transposed operand.
+    return oatt.blockwise_causal_attention(q, k.transpose(1, 2).reshape(k.shape), v,
+                                           kv_cache, cache_len, bb, scale)
+
+
+@pytest.mark.parametrize("planted", [_planted_scale_dropped, _planted_mask_one_block_late,
+                                     _planted_kt_not_transposed])
+def test_brute_force_pin_catches_planted_mistakes(planted):
+    inp = _c0_inputs()
+    bb = torch.tensor([0, 16, 32])
+    got = planted(inp.q, inp.k, inp.v, None, 0, bb, None)
+    ref = brute.attention(inp.q.numpy(), inp.k.numpy(), inp.v.numpy(), starts=[0, 16, 32])
+    assert not np.allclose(got.numpy(), ref, atol=1e-3)
+
+
+def test_rounding_pin_catches_a_lost_rounding_step():
+    q, k, w, cos, sin = _rope_inputs(l=16, h=4, d=32)
+    no_round = brute.qk_norm_rope(q.float().numpy(), w.float().numpy(), cos.numpy(), sin.numpy(),
+                                  1e-6, True)
+    got, _ = orope.qk_norm_rope(q, k, w, w, cos, sin, 1e-6, True, keep_fp32=True)
+    # Without the reference's bf16 rounding after the norm the fp32 results
+    # differ by far more than fp32 arithmetic noise.
+    assert np.quantile(np.abs(got.numpy() - no_round), 0.5) > 1e-4
+
+
+def test_scale_default_is_inverse_sqrt_head_dim():
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(1, 8, 1, 16, generator=g) for _ in range(3))
+    a = oatt.blockwise_causal_attention(q, k, v)
+    b = oatt.blockwise_causal_attention(q, k, v, softmax_scale=1 / math.sqrt(16))
+    assert torch.equal(a, b)
