@@ -20,24 +20,42 @@
 // and V^T is staged in LDS with each 16-key group stored in the order
 // [0-3, 8-11, 4-7, 12-15] so each A operand is one 16-byte LDS read.
 //
-// Masking. Per workgroup the host-independent bounds kv_min / kv_max (over its
-// queries' visible-key ends, read from block_starts on the device) split the
-// key tiles into three kinds: tiles below kv_min need no mask, tiles from
-// kv_max on are never visited (whole future blocks are skipped), and only the
-// straddling tiles are masked elementwise. Rows at or beyond kv_max are
-// zero-filled in LDS instead of loaded, so nothing a workgroup cannot see
-// reaches its arithmetic.
+// Softmax. Exponentials are v_exp_f32 on fma(score, scale*log2e, -ref).
+// The reference max is refreshed lazily: only when some lane's max grows by
+// more than 2^8 does the wave rescale its accumulators, so most tiles do no
+// rescale work (exponentials stay <= 256, exact in fp32 and in the 16-bit P).
 //
-// Work decomposition. One workgroup = NW waves = 32*NW queries of one
-// (batch, head), over one contiguous range of key tiles. Short query chunks
-// over long caches (decode) split the key range over several workgroups
-// (split-KV) and a second kernel merges the partial (max, sum, acc) triples.
-// Workgroups are issued heaviest-first (latest query tile first), and when
-// B*H is a multiple of 8 all workgroups of one (batch, head) land on the same
-// XCD (workgroup i runs on XCD i % 8), so that head's K/V is shared through
-// one L2.
+// Masking. Per workgroup the bounds kv_min / kv_max (over its queries'
+// visible-key ends, derived on the device from block_starts) split the key
+// tiles into three kinds: tiles below kv_min need no mask, tiles from kv_max on
+// are never visited (whole future blocks are skipped), and only the straddling
+// tiles are masked elementwise. Rows at or beyond kv_max are zero-filled in
+// LDS instead of loaded, so nothing a workgroup cannot see reaches its
+// arithmetic.
+//
+// Pipeline. A stream is four waves (128 queries); waves whose 32 queries
+// are all past the end only help load. K/V tiles of 64 keys go global ->
+// registers -> LDS (double buffered, one barrier per tile), the next tile's
+// loads in flight behind the current tile's compute. Prefill runs one stream
+// per workgroup, two workgroups per CU. Decode-shaped calls (short query
+// chunk, long cache) run two streams per workgroup on alternate tiles of the
+// same key range -- two waves per SIMD, so one stream's softmax overlaps the
+// other's MFMAs -- and merge them through LDS, halving the split-KV partials
+// two separate workgroups would write.
+//
+// Work decomposition. A work item is (batch, head, query tile, key split).
+// Short query chunks over long caches split the key range over several
+// workgroups (split-KV) and a second kernel merges the partial
+// (max, sum, acc) triples. Items are issued heaviest-first, and when the
+// number of heads per segment is a multiple of 8 every item of one head lands
+// on one XCD (item i runs on XCD i % 8), so its K/V and partials stay in one
+// L2. Ragged batches (one cache length per sequence) get one segment per
+// sequence with its own split count, longest sequence first.
 #include "dx_common.h"
 
+#include <stdlib.h>
+
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -45,7 +63,10 @@ namespace dx {
 namespace {
 
 constexpr int kBN = 64;        // keys per tile
-constexpr int kMaxVarlen = 64; // sequences with their own cache length
+constexpr int kNW = 4;         // waves per workgroup
+constexpr int kBM = 32 * kNW;  // queries per workgroup
+constexpr int kMaxSeg = 64;    // sequences with their own cache length
+constexpr int kMaxSplits = 16;
 
 struct AttnArgs {
   const uint16_t* q; int64_t q_sb, q_sl, q_sh;
@@ -53,14 +74,23 @@ struct AttnArgs {
   const uint16_t* v; int64_t v_sb, v_sl, v_sh;
   const uint16_t* ck; const uint16_t* cv; int64_t c_sb, c_ss, c_sh;
   uint16_t* out; int64_t o_sb, o_sl, o_sh;
-  float* ws_o;   // [partials][32*NW][D] unnormalised accumulators
-  float* ws_ml;  // [partials][32*NW][2]  (running max, running sum)
+  float* ws_o;   // [partials][kBM][D] unnormalised accumulators
+  float* ws_ml;  // [partials][kBM][2]  (exponent reference in log2 units, sum)
   const void* starts; int starts_i64; int n_blocks;
   int B, H, Lq, Lk;
   int causal;
-  int n_qtiles, n_splits, xcd_map;
-  float scale_log2;  // softmax scale * log2(e)
-  int varlen; int cache_len; int cache_lens[kMaxVarlen];
+  int n_qtiles;
+  float scale_log2;  // |softmax scale| * log2(e)
+  int negate_q;      // softmax scale < 0: q enters negated (exact), scale as |scale|
+  int cache_len;     // uniform mode
+  int n_splits;      // uniform mode
+  // Segment table (ragged batches): segment i covers sequence seg_b[i] with
+  // seg_splits[i] splits, work items [seg_base[i], seg_base[i+1]) and combine
+  // blocks [comb_base[i], comb_base[i+1]). n_seg == 0: one uniform segment
+  // over all B*H (batch, head) pairs.
+  int n_seg;
+  int seg_b[kMaxSeg], seg_splits[kMaxSeg], seg_cache[kMaxSeg];
+  int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
 };
 
 template <typename T> struct Mfma;
@@ -87,6 +117,8 @@ template <> struct Mfma<f16_t> {
   }
 };
 
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ int load_start(const AttnArgs& a, int i) {
   return a.starts_i64 ? int(static_cast<const int64_t*>(a.starts)[i])
                       : static_cast<const int32_t*>(a.starts)[i];
@@ -106,252 +138,346 @@ __device__ __forceinline__ int visible_end(const AttnArgs& a, int i) {
   return min(e, a.Lq);
 }
 
-// LDS geometry: K rows padded by 8 elements (272 B for D=128: 16-lane
-// groups of 16-byte reads hit 64 distinct banks); V^T rows of 64 keys padded
-// to 72 elements (144 B) for the same reason.
+// LDS geometry, per stage: a K tile [64 keys][D] and a V tile [64 keys][D],
+// both row-major as they lie in memory.
+//  - K rows are padded by 8 elements (272 B for D=128): the QK^T A operand is
+//    a 16-byte read of 16 different rows per pass, which then hit 64
+//    distinct banks.
+//  - V rows are padded by 32 elements (320 B for D=128, 192 B for D=64; a
+//    pitch of 16 mod 64 dwords): the PV A operand comes from
+//    ds_read_b64_tr_b16, each of which touches 8 rows x 16 dwords, and with
+//    this pitch those spans tile the 64 banks exactly twice (the minimum).
 template <int D> struct Lds {
   static constexpr int kPitch = D + 8;
-  static constexpr int vPitch = kBN + 8;
+  static constexpr int vPitch = D + 32;
   static constexpr int kElems = kBN * kPitch;
-  static constexpr int vElems = D * vPitch;
+  static constexpr int vElems = kBN * vPitch;
+  static constexpr int stage = kElems + vElems;  // one K tile + one V tile
+  static constexpr int bytes = 2 * stage * 2;    // double buffered, 16-bit elements
+  static_assert(bytes >= 4 * (2 + D / 2) * 64 * kNW,
+                "a stream's region must hold the (max, sum, acc) hand-over");
 };
 
-template <int NW, int D>
+// One K tile and one V tile of a workgroup's share, staged in registers
+// between the global load and the LDS store. Thread x moves 16-byte chunks
+// x, x + 256, ... of each tile: 16 consecutive threads cover one 256-byte
+// key row, so every load instruction reads whole rows.
+template <int D>
 struct TileRegs {
-  static constexpr int NT = 64 * NW;
-  static constexpr int KCH = kBN * D / 8;  // 16-byte chunks of a K tile
-  static constexpr int KPT = (KCH + NT - 1) / NT;
-  static constexpr int VG = 16 * D / 8;    // 4-key x 8-dim groups of a V tile
-  static constexpr int VPT = (VG + NT - 1) / NT;
-  u32x4 kr[KPT];
-  u32x4 vr[VPT][4];
+  static constexpr int NT = 64 * kNW;
+  static constexpr int CPR = D / 8;        // 16-byte chunks per key row
+  static constexpr int CH = kBN * CPR;     // chunks per tile
+  static constexpr int CPT = CH / NT;      // chunks per thread
+  static_assert(CH % NT == 0, "tile must split evenly over the threads");
+  u32x4 kr[CPT], vr[CPT];
 
-  __device__ __forceinline__ void load(const uint16_t* kc, const uint16_t* kn,
+  // Rows at or past kv_max are zero-filled, never read.
+  __device__ __forceinline__ void load(int tid, const uint16_t* kc, const uint16_t* kn,
                                        const uint16_t* vc, const uint16_t* vn,
                                        int64_t c_ss, int64_t k_sl, int64_t v_sl,
                                        int cache_len, int kv_max, int j0) {
-    const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int c = tid + i * NT;
+      const int j = j0 + c / CPR, col = (c % CPR) * 8;
       kr[i] = u32x4{0, 0, 0, 0};
-      if (c < KCH) {
-        const int row = c / (D / 8), col = c % (D / 8);
-        const int j = j0 + row;
-        if (j < kv_max) {
-          const uint16_t* p = j < cache_len ? kc + j * c_ss : kn + (j - cache_len) * k_sl;
-          kr[i] = *reinterpret_cast<const u32x4*>(p + col * 8);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int x = tid + i * NT;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vr[i][r] = u32x4{0, 0, 0, 0};
-      if (x < VG) {
-        const int kg = x % 16, dg = x / 16;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = j0 + 4 * kg + r;
-          if (j < kv_max) {
-            const uint16_t* p = j < cache_len ? vc + j * c_ss : vn + (j - cache_len) * v_sl;
-            vr[i][r] = *reinterpret_cast<const u32x4*>(p + dg * 8);
-          }
-        }
+      vr[i] = u32x4{0, 0, 0, 0};
+      if (j < kv_max) {
+        const bool cached = j < cache_len;
+        const uint16_t* pk = cached ? kc + j * c_ss : kn + (j - cache_len) * k_sl;
+        const uint16_t* pv = cached ? vc + j * c_ss : vn + (j - cache_len) * v_sl;
+        kr[i] = *reinterpret_cast<const u32x4*>(pk + col);
+        vr[i] = *reinterpret_cast<const u32x4*>(pv + col);
       }
     }
   }
 
-  __device__ __forceinline__ void store(uint16_t* Ks, uint16_t* Vt) const {
-    const int tid = threadIdx.x;
+  __device__ __forceinline__ void store(int tid, uint16_t* Ks, uint16_t* Vs) const {
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       const int c = tid + i * NT;
-      if (c < KCH) {
-        const int row = c / (D / 8), col = c % (D / 8);
-        *reinterpret_cast<u32x4*>(Ks + row * Lds<D>::kPitch + col * 8) = kr[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int x = tid + i * NT;
-      if (x < VG) {
-        const int kg = x % 16, dg = x / 16;
-        const int qd = kg % 4;
-        const int phys = 16 * (kg / 4) + 8 * (qd % 2) + 4 * (qd / 2);
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-          const int w = d / 2;
-          uint32_t lo, hi;
-          if (d % 2 == 0) {
-            lo = (vr[i][0][w] & 0xffffu) | (vr[i][1][w] << 16);
-            hi = (vr[i][2][w] & 0xffffu) | (vr[i][3][w] << 16);
-          } else {
-            lo = (vr[i][0][w] >> 16) | (vr[i][1][w] & 0xffff0000u);
-            hi = (vr[i][2][w] >> 16) | (vr[i][3][w] & 0xffff0000u);
-          }
-          *reinterpret_cast<u32x2*>(Vt + (dg * 8 + d) * Lds<D>::vPitch + phys) = u32x2{lo, hi};
-        }
-      }
+      const int row = c / CPR, col = (c % CPR) * 8;
+      *reinterpret_cast<u32x4*>(Ks + row * Lds<D>::kPitch + col) = kr[i];
+      *reinterpret_cast<u32x4*>(Vs + row * Lds<D>::vPitch + col) = vr[i];
     }
   }
 };
 
-struct Item { int b, h, qtile, split; };
-
-__device__ __forceinline__ Item decode_item(const AttnArgs& a, int item) {
-  const int nbh = a.B * a.H;
-  int bh, r;
-  if (a.xcd_map) {
-    const int xcd = item & 7, slot = item >> 3, g8 = nbh >> 3;
-    bh = xcd + 8 * (slot % g8);
-    r = slot / g8;
-  } else {
-    bh = item % nbh;
-    r = item / nbh;
-  }
-  Item it;
-  it.b = bh / a.H;
-  it.h = bh % a.H;
-  it.split = r % a.n_splits;
-  it.qtile = a.n_qtiles - 1 - r / a.n_splits;
-  return it;
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each group of 16
+// lanes, lane i receives element i % 4 of the 8-byte chunks addressed by
+// lanes 4e + i / 4, e = 0..3 of its group.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)((__attribute__((address_space(3))) uint16_t*)(p)));
+  return __builtin_bit_cast(u32x2, r);
 }
 
-template <int NW, int D, typename T>
-__global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(AttnArgs a) {
-  constexpr int BM = 32 * NW;
+// Position of a work item (or of a combine block) in the schedule.
+struct Coord {
+  int b, h, qtile, split;  // split: key split (work items) or row chunk (combine)
+  int n_splits, cache_len;
+  int64_t pbase;           // partial index of split 0 of this (b, h, qtile)
+};
+
+// Map index i of a range laid out as [groups G][ranks R] with XCD-aware
+// interleaving: when G % 8 == 0, index i runs on XCD i % 8 and all ranks of
+// group g share XCD g % 8.
+__device__ __forceinline__ void split_index(int i, int G, int& gidx, int& rank) {
+  if ((G & 7) == 0) {
+    const int xcd = i & 7, slot = i >> 3, g8 = G >> 3;
+    gidx = xcd + 8 * (slot % g8);
+    rank = slot / g8;
+  } else {
+    gidx = i % G;
+    rank = i / G;
+  }
+}
+
+// per_q: ranks per query tile (key splits for work items, row chunks for the
+// combine); base: the segment table column (seg_base or comb_base).
+__device__ __forceinline__ Coord locate(const AttnArgs& a, int idx, bool combine, int chunks) {
+  Coord c;
+  int G, local, seg_item_base;
+  if (a.n_seg == 0) {
+    G = a.B * a.H;
+    c.n_splits = a.n_splits;
+    c.cache_len = a.cache_len;
+    local = idx;
+    seg_item_base = 0;
+  } else {
+    const int* base = combine ? a.comb_base : a.seg_base;
+    int s = 0;
+    while (s + 1 < a.n_seg && idx >= base[s + 1]) ++s;
+    G = a.H;
+    c.n_splits = a.seg_splits[s];
+    c.cache_len = a.seg_cache[s];
+    local = idx - base[s];
+    seg_item_base = a.seg_base[s];
+    c.b = a.seg_b[s];
+  }
+  const int per_q = combine ? chunks : c.n_splits;
+  int gidx, rank;
+  split_index(local, G, gidx, rank);
+  c.split = rank % per_q;
+  c.qtile = a.n_qtiles - 1 - rank / per_q;  // heaviest (latest) query tiles first
+  if (a.n_seg == 0) {
+    c.b = gidx / a.H;
+    c.h = gidx % a.H;
+  } else {
+    c.h = gidx;
+  }
+  c.pbase = seg_item_base + (int64_t(gidx) * a.n_qtiles + c.qtile) * c.n_splits;
+  return c;
+}
+
+// Online-softmax state of one lane (one query; lanes l and l^32 share it).
+struct Softmax {
+  float m;  // max of raw scores so far: the exponent reference (possibly stale)
+  float l;  // sum of exponentials (this lane's half of the keys)
+};
+
+// One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// ``full`` = every key of the tile is visible to every query of the workgroup.
+template <int D, typename T>
+__device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs,
+                                          const u32x4 (&qr)[D / 16], f32x16 (&acc)[D / 32],
+                                          Softmax& sm, float c, int j0, int my_end, bool full,
+                                          int lane) {
+  constexpr int KS = D / 16, DT = D / 32;
+  const int n = lane & 31, g = lane >> 5;
+  f32x16 s[2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    s[kt] = f32x16{};
+    const uint16_t* kp = Ks + (32 * kt + n) * Lds<D>::kPitch + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      s[kt] = Mfma<T>::run(*reinterpret_cast<const u32x4*>(kp + 16 * ks), qr[ks], s[kt]);
+  }
+  // Row max over the visible scores (raw units; c >= 0 keeps the order).
+  float tmax = -INFINITY;
+  if (full) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = j0 + 32 * kt + 8 * (r / 4) + 4 * g + (r % 4);
+        tmax = fmaxf(tmax, key < my_end ? s[kt][r] : -INFINITY);
+      }
+  }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const float m_new = fmaxf(sm.m, tmax);
+  // Lazy rescale (wave-uniform branch). First visible tile: m = -inf, always.
+  const bool grow = (m_new - sm.m) * c > 8.0f;
+  if (__any(grow)) {
+    const float corr = sm.m == -INFINITY ? 0.f : fast_exp2((sm.m - m_new) * c);
+    sm.l *= corr;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) acc[d] *= corr;
+    sm.m = m_new;
+  }
+  // Nothing visible yet: exponent base 0; masked p are set to 0 below.
+  const float mb = sm.m == -INFINITY ? 0.f : sm.m * c;
+  float psum = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = fast_exp2(__builtin_fmaf(s[kt][r], c, -mb));
+      if (!full) {
+        const int key = j0 + 32 * kt + 8 * (r / 4) + 4 * g + (r % 4);
+        p = key < my_end ? p : 0.f;
+      }
+      s[kt][r] = p;
+      psum += p;
+    }
+  sm.l += psum;
+  // O^T += V^T P^T, 16 keys per MFMA (key step u = 2 kt + hf). The A
+  // operand of lane (n, g) is head_dim column 32 d + n at keys
+  // 16u + {4g..4g+3, 8+4g..8+4g+3}, gathered from the row-major V tile by two
+  // transposing reads: lane j of each 16-lane group addresses key
+  // 16u + 8r + 4g + j/4 (r = 0, 1) at dims 32 d + 16 ((lane/16) % 2) + 4 (j % 4).
+  const int j = lane & 15, half = (lane >> 4) & 1;
+  const uint16_t* vbase = Vs + (4 * g + (j >> 2)) * Lds<D>::vPitch + 16 * half + 4 * (j & 3);
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      u32x4 pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pb[e] = Mfma<T>::pack(s[kt][8 * hf + 2 * e], s[kt][8 * hf + 2 * e + 1]);
+      const uint16_t* vu = vbase + 16 * (2 * kt + hf) * Lds<D>::vPitch;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        const u32x2 lo = lds_read_tr16(vu + 32 * d);
+        const u32x2 hi = lds_read_tr16(vu + 8 * Lds<D>::vPitch + 32 * d);
+        acc[d] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, acc[d]);
+      }
+    }
+}
+
+template <int D, typename T, int NS>
+__global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
   constexpr int DT = D / 32;  // 32-wide head_dim tiles of the output
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[Lds<D>::kElems];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[Lds<D>::vElems];
-  __shared__ int red_min[NW], red_max[NW];
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 
-  const Item it = decode_item(a, blockIdx.x);
+  const Coord it = locate(a, blockIdx.x, false, 0);
   const int b = it.b, h = it.h;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // NS streams of four waves; stream s takes every NS-th tile of the range.
+  const int stream = NS == 1 ? 0 : int(threadIdx.x) / (64 * kNW);
+  const int ltid = int(threadIdx.x) - stream * 64 * kNW;
+  const int wave = ltid >> 6, lane = ltid & 63;
   const int g = lane >> 5, n = lane & 31;
-  const int qi = it.qtile * BM + wave * 32 + n;
+  const int q0 = it.qtile * kBM;
+  const int qi = q0 + wave * 32 + n;
   const bool qvalid = qi < a.Lq;
-  const int cache_len = a.varlen ? a.cache_lens[b] : a.cache_len;
+  const bool wave_active = q0 + wave * 32 < a.Lq;
+  const int cache_len = it.cache_len;
 
-  // Visible-key end of this lane's query, and the workgroup's bounds.
-  const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
-  int vmin = qvalid ? my_end : 0x7fffffff, vmax = my_end;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    vmin = min(vmin, __shfl_xor(vmin, off, 64));
-    vmax = max(vmax, __shfl_xor(vmax, off, 64));
-  }
-  if (lane == 0) { red_min[wave] = vmin; red_max[wave] = vmax; }
-  __syncthreads();
-  int kv_min = red_min[0], kv_max = red_max[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) { kv_min = min(kv_min, red_min[w]); kv_max = max(kv_max, red_max[w]); }
+  // Key range of the workgroup. Block starts are sorted ascending, so the
+  // visible end is non-decreasing in the query index: the first and last
+  // queries bound it. Workgroup-uniform (scalar) work, no barrier, so the
+  // tile loads below go out right away.
+  const int kv_min = cache_len + visible_end(a, q0);
+  const int kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
 
   const int n_tiles = (kv_max + kBN - 1) / kBN;
-  const int t_begin = int((int64_t(it.split) * n_tiles) / a.n_splits);
-  const int t_end = int((int64_t(it.split + 1) * n_tiles) / a.n_splits);
-
-  // Q^T operand: lane holds query n, head_dim [16s + 8g, 16s + 8g + 8) per k-step s.
-  u32x4 qr[KS];
-  {
-    const uint16_t* qp = a.q + b * a.q_sb + int64_t(qi) * a.q_sl + h * a.q_sh;
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qr[s] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * g) : u32x4{0, 0, 0, 0};
-  }
+  const int t_begin = int((int64_t(it.split) * n_tiles) / it.n_splits);
+  const int t_end = int((int64_t(it.split + 1) * n_tiles) / it.n_splits);
+  const int iters = (t_end - t_begin + NS - 1) / NS;  // barrier rounds, equal for all streams
 
   const uint16_t* kc = a.ck + b * a.c_sb + h * a.c_sh;
   const uint16_t* vc = a.cv + b * a.c_sb + h * a.c_sh;
   const uint16_t* kn = a.k + b * a.k_sb + h * a.k_sh;
   const uint16_t* vn = a.v + b * a.v_sb + h * a.v_sh;
 
+  // Request this stream's first tile before anything waits on memory.
+  TileRegs<D> regs;
+  const int t_first = t_begin + stream;
+  if (t_first < t_end)
+    regs.load(ltid, kc, kn, vc, vn, a.c_ss, a.k_sl, a.v_sl, cache_len, kv_max, t_first * kBN);
+
+  // Visible-key end of this lane's query (per-key masking of straddling tiles).
+  const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
+
+  // Q^T operand: lane holds query n, head_dim [16s + 8g, 16s + 8g + 8) per k-step s.
+  u32x4 qr[KS];
+  {
+    const uint16_t* qp = a.q + b * a.q_sb + int64_t(qi) * a.q_sl + h * a.q_sh;
+    const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qr[s] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * g) : u32x4{0, 0, 0, 0};
+      qr[s] ^= flip;
+    }
+  }
+
   f32x16 acc[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  Softmax sm{-INFINITY, 0.f};
+  const float c = a.scale_log2;
 
-  TileRegs<NW, D> regs;
-  if (t_begin < t_end)
-    regs.load(kc, kn, vc, vn, a.c_ss, a.k_sl, a.v_sl, cache_len, kv_max, t_begin * kBN);
-
-  for (int t = t_begin; t < t_end; ++t) {
-    const int j0 = t * kBN;
-    __syncthreads();  // previous tile's LDS reads are done
-    regs.store(Ks, Vt);
+  // Each stream double-buffers its tiles in its own LDS region. A buffer is
+  // rewritten two rounds after it was read, past the barrier of the round in
+  // between, which every wave has reached.
+  uint16_t* const region = smem + stream * 2 * Lds<D>::stage;
+  for (int i = 0; i < iters; ++i) {
+    const int t = t_first + i * NS;
+    uint16_t* const st = region + (i & 1) * Lds<D>::stage;
+    if (t < t_end) regs.store(ltid, st, st + Lds<D>::kElems);
     __syncthreads();
-    if (t + 1 < t_end)
-      regs.load(kc, kn, vc, vn, a.c_ss, a.k_sl, a.v_sl, cache_len, kv_max, j0 + kBN);
-
-    // S^T tile: two 32-key halves.
-    f32x16 s[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      s[kt] = f32x16{};
-      const uint16_t* kp = Ks + (32 * kt + n) * Lds<D>::kPitch + 8 * g;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        s[kt] = Mfma<T>::run(*reinterpret_cast<const u32x4*>(kp + 16 * ks), qr[ks], s[kt]);
-    }
-
-    // Scale into the exp2 domain; mask only tiles that straddle a boundary.
-    const bool full = j0 + kBN <= kv_min;
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[kt][r] * a.scale_log2;
-        if (!full) {
-          const int key = j0 + 32 * kt + 8 * (r / 4) + 4 * g + (r % 4);
-          x = key < my_end ? x : -INFINITY;
-        }
-        s[kt][r] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    // Nothing visible yet: use 0 as the exponent base so every exp2 is of -inf
-    // (exactly 0) and never of (-inf) - (-inf).
-    const float base = m_new == -INFINITY ? 0.f : m_new;
-    const float corr = exp2f(m_run - base);
-    m_run = m_new;
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[kt][r] - base);
-        s[kt][r] = p;
-        psum += p;
-      }
-    l_run = l_run * corr + psum;
-#pragma unroll
-    for (int d = 0; d < DT; ++d) acc[d] *= corr;
-
-    // O^T += V^T P^T, 16 keys per MFMA.
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        u32x4 pb;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pb[e] = Mfma<T>::pack(s[kt][8 * hf + 2 * e], s[kt][8 * hf + 2 * e + 1]);
-        const int u = 2 * kt + hf;
-        const uint16_t* vp = Vt + n * Lds<D>::vPitch + 16 * u + 8 * g;
-#pragma unroll
-        for (int d = 0; d < DT; ++d)
-          acc[d] = Mfma<T>::run(*reinterpret_cast<const u32x4*>(vp + 32 * d * Lds<D>::vPitch),
-                                pb, acc[d]);
-      }
+    if (t + NS < t_end)
+      regs.load(ltid, kc, kn, vc, vn, a.c_ss, a.k_sl, a.v_sl, cache_len, kv_max,
+                (t + NS) * kBN);
+    if (wave_active && t < t_end)
+      tile_step<D, T>(st, st + Lds<D>::kElems, qr, acc, sm, c, t * kBN, my_end,
+                      (t + 1) * kBN <= kv_min, lane);
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  // The exponent reference of acc and l, in log2 units.
+  float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
+  if (NS == 2) {
+    // Stream 1 hands (mref, l, acc) to the same lane of stream 0 through LDS,
+    // laid out [value][lane] so consecutive lanes hit consecutive banks.
+    constexpr int LANES = 64 * kNW;
+    float* x = reinterpret_cast<float*>(smem);
+    __syncthreads();  // all tile reads done: the LDS is free
+    if (stream == 1) {
+      x[ltid] = mref;
+      x[LANES + ltid] = sm.l;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[(2 + d * 16 + r) * LANES + ltid] = acc[d][r];
+    }
+    __syncthreads();
+    if (stream == 1) return;
+    const float m1 = x[ltid], l1 = x[LANES + ltid];
+    const float mm = fmaxf(mref, m1);
+    const float base = mm == -INFINITY ? 0.f : mm;
+    const float w0 = fast_exp2(mref - base), w1 = fast_exp2(m1 - base);
+    sm.l = sm.l * w0 + l1 * w1;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        acc[d][r] = acc[d][r] * w0 + x[(2 + d * 16 + r) * LANES + ltid] * w1;
+    mref = mm;
+  }
+
+  const float l_tot = sm.l + __shfl_xor(sm.l, 32, 64);
   if (!qvalid) return;
-  if (a.n_splits == 1) {
+  if (it.n_splits == 1) {
     const float inv = 1.0f / l_tot;  // 0 visible keys: 0 * inf = NaN, as the reference
     uint16_t* op = a.out + b * a.o_sb + int64_t(qi) * a.o_sl + h * a.o_sh;
 #pragma unroll
@@ -365,10 +491,9 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(AttnArgs a) {
         *reinterpret_cast<u32x2*>(op + dim) = w;
       }
   } else {
-    const int64_t pidx =
-        (int64_t(b * a.H + h) * a.n_qtiles + it.qtile) * a.n_splits + it.split;
+    const int64_t pidx = it.pbase + it.split;
     const int row = wave * 32 + n;
-    float* po = a.ws_o + (pidx * BM + row) * D;
+    float* po = a.ws_o + (pidx * kBM + row) * D;
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
@@ -377,63 +502,64 @@ __global__ __launch_bounds__(64 * NW) void attn_fwd_kernel(AttnArgs a) {
         *reinterpret_cast<f32x4*>(po + dim) =
             f32x4{acc[d][4 * r4], acc[d][4 * r4 + 1], acc[d][4 * r4 + 2], acc[d][4 * r4 + 3]};
       }
-    if (g == 0) {
-      float* pm = a.ws_ml + (pidx * BM + row) * 2;
-      pm[0] = m_run;
-      pm[1] = l_tot;
-    }
+    if (g == 0)
+      *reinterpret_cast<float2*>(a.ws_ml + (pidx * kBM + row) * 2) = make_float2(mref, l_tot);
   }
 }
 
+template <int D> struct CombineShape {
+  static constexpr int TPR = D / 4;                   // threads per row
+  static constexpr int RPB = 256 / TPR;               // rows per block
+  static constexpr int BPT = (kBM + RPB - 1) / RPB;   // blocks per query tile
+};
+
 // Merge split-KV partials: out = sum_s w_s acc_s / sum_s w_s l_s with
-// w_s = exp2(m_s - max_s m_s). Each thread owns 4 consecutive dims of a row.
-template <int NW, int D, typename T>
+// w_s = exp2(m_s - max_s m_s). Each thread owns 4 consecutive dims of a row
+// and issues every load it needs before combining. Blocks of one
+// (batch, head) run on the XCD whose L2 holds that head's partials.
+template <int D, typename T>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  constexpr int BM = 32 * NW;
-  constexpr int TPR = D / 4;           // threads per row
-  constexpr int RPB = 256 / TPR;       // rows per block
-  constexpr int BPT = (BM + RPB - 1) / RPB;  // blocks per q-tile
-  const int blk = blockIdx.x;
-  const int chunk = blk % BPT;
-  const int rest = blk / BPT;
-  const int qtile = rest % a.n_qtiles;
-  const int bh = rest / a.n_qtiles;
-  const int row = chunk * RPB + threadIdx.x / TPR;
-  const int dim = 4 * (threadIdx.x % TPR);
-  const int qi = qtile * BM + row;
-  if (row >= BM || qi >= a.Lq) return;
-  const int b = bh / a.H, h = bh % a.H;
-  const int64_t p0 = (int64_t(bh) * a.n_qtiles + qtile) * a.n_splits;
+  using CS = CombineShape<D>;
+  const Coord cd = locate(a, blockIdx.x, true, CS::BPT);
+  const int row = cd.split * CS::RPB + threadIdx.x / CS::TPR;
+  const int dim = 4 * (threadIdx.x % CS::TPR);
+  const int qi = cd.qtile * kBM + row;
+  if (row >= kBM || qi >= a.Lq) return;
+  float2 ml[kMaxSplits];
+  f32x4 o[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    if (s < cd.n_splits) {
+      ml[s] = *reinterpret_cast<const float2*>(a.ws_ml + ((cd.pbase + s) * kBM + row) * 2);
+      o[s] = *reinterpret_cast<const f32x4*>(a.ws_o + ((cd.pbase + s) * kBM + row) * D + dim);
+    }
+  }
   float mmax = -INFINITY;
-  for (int s = 0; s < a.n_splits; ++s)
-    mmax = fmaxf(mmax, a.ws_ml[((p0 + s) * BM + row) * 2]);
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s)
+    if (s < cd.n_splits) mmax = fmaxf(mmax, ml[s].x);
   const float base = mmax == -INFINITY ? 0.f : mmax;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
-  for (int s = 0; s < a.n_splits; ++s) {
-    const float* pm = a.ws_ml + ((p0 + s) * BM + row) * 2;
-    const float w = exp2f(pm[0] - base);
-    l += w * pm[1];
-    const f32x4 x = *reinterpret_cast<const f32x4*>(a.ws_o + ((p0 + s) * BM + row) * D + dim);
-    o += w * x;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    if (s < cd.n_splits) {
+      const float w = fast_exp2(ml[s].x - base);
+      l += w * ml[s].y;
+      acc += w * o[s];
+    }
   }
   const float inv = 1.0f / l;
-  uint16_t* op = a.out + b * a.o_sb + int64_t(qi) * a.o_sl + h * a.o_sh + dim;
+  uint16_t* op = a.out + cd.b * a.o_sb + int64_t(qi) * a.o_sl + cd.h * a.o_sh + dim;
   u32x2 w2;
-  w2[0] = Mfma<T>::pack(o[0] * inv, o[1] * inv);
-  w2[1] = Mfma<T>::pack(o[2] * inv, o[3] * inv);
+  w2[0] = Mfma<T>::pack(acc[0] * inv, acc[1] * inv);
+  w2[1] = Mfma<T>::pack(acc[2] * inv, acc[3] * inv);
   *reinterpret_cast<u32x2*>(op) = w2;
 }
 
 // ---------------------------------------------------------------------------
 // Host side: launch planning shared by the workspace query and the launch.
 // ---------------------------------------------------------------------------
-struct Plan {
-  int nw, n_qtiles, n_splits;
-  int64_t items;
-  int64_t ws_bytes;
-};
-
 int device_cus() {
   static std::mutex mu;
   static std::vector<int> cache;
@@ -451,50 +577,140 @@ int device_cus() {
   return cache[dev];
 }
 
-Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t max_cache_len) {
-  Plan p{};
-  int64_t nw = (Lq + 31) / 32;
-  p.nw = int(nw < 1 ? 1 : (nw > 4 ? 4 : nw));
-  const int64_t bm = 32 * p.nw;
-  p.n_qtiles = int((Lq + bm - 1) / bm);
-  const int64_t base = B * H * p.n_qtiles;
-  const int64_t tiles = (max_cache_len + Lq + kBN - 1) / kBN;
-  const int64_t target = 2 * int64_t(device_cus());
-  int64_t splits = 1;
-  if (base > 0 && base * 4 < target * 3 && tiles >= 4) {
-    splits = (target + base - 1) / base;
-    const int64_t cap = tiles / 2;
-    if (splits > cap) splits = cap;
-    if (splits < 1) splits = 1;
+struct Plan {
+  int n_qtiles;
+  int streams;               // 2: decode-shaped (one 8-wave workgroup per CU), 1: prefill
+  int n_seg;                 // 0 = uniform
+  int uniform_splits;
+  std::vector<int> seg_b, seg_splits, seg_cache, seg_base, comb_base;
+  int64_t items, comb_blocks, partials;
+  int64_t ws_bytes;
+};
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+int64_t combine_bpt(int64_t D) {
+  return D == 128 ? CombineShape<128>::BPT : CombineShape<64>::BPT;
+}
+
+long split_override() {  // DX_ATTN_SPLITS=<n>: tuning override (measurement only)
+  const char* env = getenv("DX_ATTN_SPLITS");
+  return env ? strtol(env, nullptr, 10) : 0;
+}
+
+// Split count for `groups` (batch, head, query tile) units of `tiles` key
+// tiles each. Decode-shaped calls (few groups, long key range) get one
+// dual-stream workgroup per CU; otherwise the split minimising rounds x
+// tiles-per-split (two workgroups per CU) with a small cost per extra split
+// (partials + merge).
+int choose_uniform_splits(int64_t groups, int64_t tiles, int cus, int& streams) {
+  int64_t best_s = 1;
+  streams = 1;
+  if (groups * 2 <= cus && tiles >= 4) {
+    streams = 2;
+    best_s = std::min<int64_t>({kMaxSplits, cus / groups, cdiv(tiles, 2)});
+  } else if (groups < 2 * cus && tiles >= 8) {
+    double best = 1e30;
+    for (int64_t s = 1; s <= kMaxSplits && s <= tiles / 4; ++s) {
+      const double cost = double(cdiv(groups * s, 2 * cus)) * double(cdiv(tiles, s)) +
+                          (s > 1 ? 0.5 * double(s) + 1.0 : 0.0);
+      if (cost < best - 1e-9) { best = cost; best_s = s; }
+    }
   }
-  p.n_splits = int(splits);
-  p.items = base * splits;
-  p.ws_bytes = splits > 1 ? base * splits * bm * (D + 2) * int64_t(sizeof(float)) : 0;
+  const long forced = split_override();
+  if (forced >= 1) best_s = forced;
+  return int(std::max<int64_t>(1, std::min<int64_t>({best_s, kMaxSplits,
+                                                     std::max<int64_t>(tiles, 1)})));
+}
+
+Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
+               const int64_t* cache_lens) {
+  Plan p{};
+  p.n_qtiles = int(cdiv(Lq, kBM));
+  const int cus = device_cus();
+  const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
+  if (!cache_lens) {
+    const int64_t tiles = cdiv(cache_len + Lq, kBN);
+    p.uniform_splits = choose_uniform_splits(B * per_b, tiles, cus, p.streams);
+    p.items = B * per_b * p.uniform_splits;
+    p.partials = p.uniform_splits > 1 ? p.items : 0;
+    p.comb_blocks = p.uniform_splits > 1 ? B * per_b * combine_bpt(D) : 0;
+  } else {
+    // One segment per sequence, longest first, with splits proportional to
+    // its length: within one dual-stream workgroup per CU when that leaves
+    // <= 8 tiles per split, else within two single-stream workgroups per CU.
+    std::vector<int> order(B);
+    for (int i = 0; i < int(B); ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int x, int y) { return cache_lens[x] > cache_lens[y]; });
+    std::vector<int64_t> tiles(B);
+    int64_t total = 0;
+    for (int i = 0; i < int(B); ++i) {
+      tiles[i] = cdiv(cache_lens[i] + Lq, kBN);
+      total += tiles[i];
+    }
+    std::vector<int> splits(B, 1);
+    for (int streams = 2; streams >= 1; --streams) {
+      const double budget = double(cus * (streams == 2 ? 1 : 2)) / double(per_b);
+      int64_t worst = 0;
+      for (int i = 0; i < int(B); ++i) {
+        int64_t s = int64_t(budget * double(tiles[i]) / double(std::max<int64_t>(total, 1)));
+        s = std::max<int64_t>(1, std::min<int64_t>({s, kMaxSplits, tiles[i]}));
+        splits[i] = int(s);
+        worst = std::max(worst, cdiv(tiles[i], s));
+      }
+      p.streams = streams;
+      if (streams == 2 && worst <= 8) break;
+    }
+    const long forced = split_override();
+    if (forced >= 1)
+      for (int i = 0; i < int(B); ++i)
+        splits[i] = int(std::max<int64_t>(1, std::min<int64_t>({forced, kMaxSplits, tiles[i]})));
+    p.n_seg = int(B);
+    p.seg_base.push_back(0);
+    p.comb_base.push_back(0);
+    for (int k = 0; k < int(B); ++k) {
+      const int b = order[k];
+      p.seg_b.push_back(b);
+      p.seg_splits.push_back(splits[b]);
+      p.seg_cache.push_back(int(cache_lens[b]));
+      p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[b]));
+      p.comb_base.push_back(
+          int(p.comb_base.back() + (splits[b] > 1 ? per_b * combine_bpt(D) : 0)));
+    }
+    p.items = p.seg_base.back();
+    p.comb_blocks = p.comb_base.back();
+    p.partials = p.items;
+  }
+  p.ws_bytes = p.comb_blocks > 0 ? p.partials * kBM * (D + 2) * int64_t(sizeof(float)) : 0;
   return p;
 }
 
-template <int NW, int D, typename T>
-hipError_t launch_nw(const AttnArgs& a, const Plan& p, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_kernel<NW, D, T>), dim3(unsigned(p.items)), dim3(64 * NW), 0, st,
-                     a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.n_splits == 1) return e;
-  constexpr int RPB = 256 / (D / 4);
-  constexpr int BPT = (32 * NW + RPB - 1) / RPB;
-  const int64_t blocks = int64_t(a.B) * a.H * p.n_qtiles * BPT;
-  hipLaunchKernelGGL((attn_combine_kernel<NW, D, T>), dim3(unsigned(blocks)), dim3(256), 0, st,
-                     a);
+template <int D, typename T, int NS>
+hipError_t launch_main(const AttnArgs& a, int64_t items, hipStream_t st) {
+  // The double-buffered tiles exceed the 64 KB default LDS window: opt in
+  // once per instantiation (gfx950 allows 160 KB per workgroup).
+  constexpr int lds = NS * Lds<D>::bytes;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<D, T, NS>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  });
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((attn_fwd_kernel<D, T, NS>), dim3(unsigned(items)), dim3(64 * kNW * NS),
+                     lds, st, a);
   return hipGetLastError();
 }
 
 template <int D, typename T>
 hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
-  switch (p.nw) {
-    case 1: return launch_nw<1, D, T>(a, p, st);
-    case 2: return launch_nw<2, D, T>(a, p, st);
-    case 3: return launch_nw<3, D, T>(a, p, st);
-    default: return launch_nw<4, D, T>(a, p, st);
-  }
+  hipError_t e = p.streams == 2 ? launch_main<D, T, 2>(a, p.items, st)
+                                : launch_main<D, T, 1>(a, p.items, st);
+  if (e != hipSuccess || p.comb_blocks == 0) return e;
+  hipLaunchKernelGGL((attn_combine_kernel<D, T>), dim3(unsigned(p.comb_blocks)), dim3(256), 0,
+                     st, a);
+  return hipGetLastError();
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -521,15 +737,14 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   DX_CHECK_ARG(starts_dtype == DX_I32 || starts_dtype == DX_I64 || n_blocks == 0,
                "attention: block_boundaries must be int32 or int64");
   if (cache_lens) {
-    DX_CHECK_ARG(B <= kMaxVarlen, "attention varlen: B=%lld exceeds %d", (long long)B,
-                 kMaxVarlen);
+    DX_CHECK_ARG(B <= kMaxSeg, "attention varlen: B=%lld exceeds %d", (long long)B, kMaxSeg);
   }
   int64_t max_cache = cache_len;
   if (cache_lens) {
     max_cache = 0;
     for (int64_t i = 0; i < B; ++i) {
       DX_CHECK_ARG(cache_lens[i] >= 0, "attention varlen: negative cache length");
-      if (cache_lens[i] > max_cache) max_cache = cache_lens[i];
+      max_cache = std::max(max_cache, cache_lens[i]);
     }
   }
   DX_CHECK_ARG(max_cache >= 0, "attention: negative cache_len");
@@ -545,7 +760,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                                c_sh % 8 == 0)),
                "attention: strides must be multiples of 8 elements");
   if (B * Lq == 0) return DX_OK;
-  const Plan p = make_plan(B, Lq, H, D, max_cache);
+  const Plan p = make_plan(B, Lq, H, D, cache_len, cache_lens);
   DX_CHECK_ARG(p.items < (int64_t(1) << 31), "attention: grid too large");
   if (p.ws_bytes > 0) {
     if (!workspace || ws_bytes < p.ws_bytes) {
@@ -563,20 +778,28 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.cv = cache ? static_cast<const uint16_t*>(cache) + c_plane : nullptr;
   a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh;
   a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
-  const int64_t bm = 32 * p.nw;
-  const int64_t partials = B * H * p.n_qtiles * p.n_splits;
   a.ws_o = static_cast<float*>(workspace);
-  a.ws_ml = p.ws_bytes ? a.ws_o + partials * bm * D : nullptr;
+  a.ws_ml = p.ws_bytes ? a.ws_o + p.partials * kBM * D : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
   a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);
   a.causal = causal != 0;
-  a.n_qtiles = p.n_qtiles; a.n_splits = p.n_splits;
-  a.xcd_map = (B * H) % 8 == 0;
-  a.scale_log2 = softmax_scale * 1.4426950408889634f;
-  a.varlen = cache_lens != nullptr;
+  a.n_qtiles = p.n_qtiles;
+  // A negative scale enters as a negated q (exact) and |scale|, so the kernel
+  // only ever multiplies scores by a non-negative factor.
+  a.negate_q = softmax_scale < 0.f;
+  a.scale_log2 = fabsf(softmax_scale) * 1.4426950408889634f;
   a.cache_len = int(cache_len);
-  if (cache_lens)
-    for (int64_t i = 0; i < B; ++i) a.cache_lens[i] = int(cache_lens[i]);
+  a.n_splits = p.uniform_splits;
+  a.n_seg = p.n_seg;
+  for (int i = 0; i < p.n_seg; ++i) {
+    a.seg_b[i] = p.seg_b[i];
+    a.seg_splits[i] = p.seg_splits[i];
+    a.seg_cache[i] = p.seg_cache[i];
+  }
+  for (int i = 0; i <= p.n_seg && p.n_seg > 0; ++i) {
+    a.seg_base[i] = p.seg_base[i];
+    a.comb_base[i] = p.comb_base[i];
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (D == 128)
@@ -625,11 +848,19 @@ extern "C" int dx_blockwise_causal_attention_varlen(
 }
 
 extern "C" int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
-                                                int64_t D, int64_t max_cache_len) {
-  if (B < 0 || Lq < 0 || H <= 0 || (D != 64 && D != 128) || max_cache_len < 0 || Lk != Lq) {
+                                                int64_t D, int64_t cache_len,
+                                                const int64_t* cache_lens) {
+  if (B < 0 || Lq < 0 || H <= 0 || (D != 64 && D != 128) || cache_len < 0 || Lk != Lq ||
+      (cache_lens && B > kMaxSeg)) {
     set_error("attention_workspace_bytes: bad shape");
     return -DX_EINVAL;
   }
+  if (cache_lens)
+    for (int64_t i = 0; i < B; ++i)
+      if (cache_lens[i] < 0) {
+        set_error("attention_workspace_bytes: negative cache length");
+        return -DX_EINVAL;
+      }
   if (B * Lq == 0) return 0;
-  return make_plan(B, Lq, H, D, max_cache_len).ws_bytes;
+  return make_plan(B, Lq, H, D, cache_len, cache_lens).ws_bytes;
 }

@@ -29,13 +29,10 @@ __device__ __forceinline__ float to_f32(f16_t x) {
 }
 __device__ __forceinline__ float to_f32(float x) { return x; }
 
-// Round-to-nearest-even float -> bf16, NaN kept quiet (same rounding torch's
-// .to(torch.bfloat16) performs).
+// Round-to-nearest-even float -> bf16 (gfx950 v_cvt_pk_bf16_f32; the same
+// rounding torch's .to(torch.bfloat16) performs; NaN stays NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));

@@ -10,23 +10,28 @@
 // Keeping the reference's intermediate rounding makes this kernel agree with
 // the oracle to within the summation order of the mean.
 //
-// Work layout: one workgroup per (batch, token). A thread owns "units" of 8
-// rotary pairs: 16 consecutive elements when pairs are interleaved (2j, 2j+1),
-// or 8 elements at offset o plus 8 at o + D/2 for split-half pairs. Each unit
-// is two 16-byte loads per tensor, so the plane is read exactly once, with
-// the sum of squares reduced across the workgroup through LDS.
+// Work layout: one workgroup per (batch, token), one thread per "unit" of 8
+// rotary pairs: 16 consecutive elements when pairs are interleaved
+// (2j, 2j+1), or 8 elements at offset o plus 8 at o + D/2 for split-half
+// pairs. The workgroup is the unit count rounded up to whole waves (192
+// threads for a 3072-wide plane). The kernel is latency-bound at decode
+// sizes, so every global load a thread needs -- q, k, both weights, cos, sin
+// (and v for the cache write) -- is issued before the sum-of-squares
+// reduction: one memory round trip, then LDS, then the stores.
 #include "dx_common.h"
 
 namespace dx {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kMaxUnits = 4;  // H*D <= kThreads * kMaxUnits * 16 = 16384
+constexpr int kMaxThreads = 1024;  // H*D <= 1024 units * 16 = 16384
 
 template <typename W> struct Vec8;
 template <> struct Vec8<bf16_t> {
-  static __device__ __forceinline__ void load(const void* p, float (&o)[8]) {
-    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+  typedef u32x4 raw;
+  static __device__ __forceinline__ raw load(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+  }
+  static __device__ __forceinline__ void unpack(const raw& r, float (&o)[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       o[2 * i] = __uint_as_float(r[i] << 16);
@@ -35,8 +40,11 @@ template <> struct Vec8<bf16_t> {
   }
 };
 template <> struct Vec8<f16_t> {
-  static __device__ __forceinline__ void load(const void* p, float (&o)[8]) {
-    u32x4 r = *reinterpret_cast<const u32x4*>(p);
+  typedef u32x4 raw;
+  static __device__ __forceinline__ raw load(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+  }
+  static __device__ __forceinline__ void unpack(const raw& r, float (&o)[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       o[2 * i] = to_f32(f16_t{uint16_t(r[i] & 0xffffu)});
@@ -44,32 +52,31 @@ template <> struct Vec8<f16_t> {
     }
   }
 };
+struct F32x8 { f32x4 a, b; };
 template <> struct Vec8<float> {
-  static __device__ __forceinline__ void load(const void* p, float (&o)[8]) {
-    f32x4 a = reinterpret_cast<const f32x4*>(p)[0];
-    f32x4 b = reinterpret_cast<const f32x4*>(p)[1];
+  typedef F32x8 raw;
+  static __device__ __forceinline__ raw load(const void* p) {
+    return F32x8{reinterpret_cast<const f32x4*>(p)[0], reinterpret_cast<const f32x4*>(p)[1]};
+  }
+  static __device__ __forceinline__ void unpack(const raw& r, float (&o)[8]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { o[i] = a[i]; o[4 + i] = b[i]; }
+    for (int i = 0; i < 4; ++i) { o[i] = r.a[i]; o[4 + i] = r.b[i]; }
   }
 };
 
 // Round a float to the io type and back, as ``.to(x.dtype)`` then ``.float()``.
 template <typename IO>
 __device__ __forceinline__ float round_io(float x) {
-  uint16_t b = Store<IO>::bits(x);
-  return to_f32(IO{b});
+  return to_f32(IO{Store<IO>::bits(x)});
 }
 
-__device__ __forceinline__ float block_sum(float v, float* red) {
+template <typename IO>
+__device__ __forceinline__ void unpack16(const u32x4& r, float (&o)[8]) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) s += red[w];
-  return s;
+  for (int j = 0; j < 4; ++j) {
+    o[2 * j] = to_f32(IO{uint16_t(r[j] & 0xffffu)});
+    o[2 * j + 1] = to_f32(IO{uint16_t(r[j] >> 16)});
+  }
 }
 
 struct RopeArgs {
@@ -85,159 +92,158 @@ struct RopeArgs {
   float eps;
 };
 
-// Element offsets (within one head) of the lo and hi halves of unit u's pairs.
-template <bool INTERLEAVED>
-__device__ __forceinline__ void unit_offsets(int unit_in_head, int D, int& lo, int& hi) {
-  if (INTERLEAVED) { lo = unit_in_head * 16; hi = lo + 8; }
-  else { lo = unit_in_head * 8; hi = lo + D / 2; }
-}
-
 template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND>
-__global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(RopeArgs a) {
-  __shared__ float red[2][kThreads / 64];
+__global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
+  __shared__ float red[2][kMaxThreads / 64];
   const int token = blockIdx.x;  // b * L + l
   const int b = token / a.L, l = token % a.L;
   const int units_per_head = a.D / 16;
   const int n_units = a.H * units_per_head;
-  const int HD = a.H * a.D;
+  const int u = threadIdx.x;
+  const bool active = u < n_units;
+  const int h = active ? u / units_per_head : 0;
+  const int uh = active ? u % units_per_head : 0;
+  // Element offsets (within one head) of the lo and hi halves of this unit.
+  const int lo = INTERLEAVED ? uh * 16 : uh * 8;
+  const int hi = INTERLEAVED ? lo + 8 : lo + a.D / 2;
+  const int j0 = INTERLEAVED ? uh * 8 : lo;  // first rotary pair index
 
-  u32x4 qa[kMaxUnits][2], ka[kMaxUnits][2];
-  float sq = 0.f, sk = 0.f;
-#pragma unroll
-  for (int i = 0; i < kMaxUnits; ++i) {
-    const int u = threadIdx.x + i * kThreads;
-    if (u < n_units) {
-      const int h = u / units_per_head, uh = u % units_per_head;
-      int lo, hi;
-      unit_offsets<INTERLEAVED>(uh, a.D, lo, hi);
-      const uint16_t* qp = a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh;
-      const uint16_t* kp = a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh;
-      qa[i][0] = *reinterpret_cast<const u32x4*>(qp + lo);
-      qa[i][1] = *reinterpret_cast<const u32x4*>(qp + hi);
-      ka[i][0] = *reinterpret_cast<const u32x4*>(kp + lo);
-      ka[i][1] = *reinterpret_cast<const u32x4*>(kp + hi);
-#pragma unroll
-      for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float x0 = to_f32(IO{uint16_t(qa[i][p][j] & 0xffffu)});
-          float x1 = to_f32(IO{uint16_t(qa[i][p][j] >> 16)});
-          float y0 = to_f32(IO{uint16_t(ka[i][p][j] & 0xffffu)});
-          float y1 = to_f32(IO{uint16_t(ka[i][p][j] >> 16)});
-          sq += x0 * x0 + x1 * x1;
-          sk += y0 * y0 + y1 * y1;
-        }
+  // ---- every load up front ------------------------------------------------
+  u32x4 qa[2] = {}, ka[2] = {}, va[2] = {};
+  typename Vec8<W>::raw wq[2] = {}, wk[2] = {};
+  typename Vec8<TB>::raw cr = {}, sr = {};
+  if (active) {
+    const uint16_t* qp = a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh;
+    qa[0] = *reinterpret_cast<const u32x4*>(qp + lo);
+    qa[1] = *reinterpret_cast<const u32x4*>(qp + hi);
+    ka[0] = *reinterpret_cast<const u32x4*>(kp + lo);
+    ka[1] = *reinterpret_cast<const u32x4*>(kp + hi);
+    wq[0] = Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + lo);
+    wq[1] = Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + hi);
+    wk[0] = Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + lo);
+    wk[1] = Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + hi);
+    cr = Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0);
+    sr = Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0);
+    if (APPEND) {
+      const uint16_t* vp = a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
+      va[0] = *reinterpret_cast<const u32x4*>(vp + lo);
+      va[1] = *reinterpret_cast<const u32x4*>(vp + hi);
     }
   }
-  const float tq = block_sum(sq, red[0]);
-  const float tk = block_sum(sk, red[1]);
-  const float rq = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tq, float(HD)) + a.eps));
-  const float rk = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tk, float(HD)) + a.eps));
 
+  // ---- sum of squares over the plane ------------------------------------
+  float xq[2][8], xk[2][8];
 #pragma unroll
-  for (int i = 0; i < kMaxUnits; ++i) {
-    const int u = threadIdx.x + i * kThreads;
-    if (u >= n_units) continue;
-    const int h = u / units_per_head, uh = u % units_per_head;
-    int lo, hi;
-    unit_offsets<INTERLEAVED>(uh, a.D, lo, hi);
-
-    float wq[2][8], wk[2][8];
-    Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + lo, wq[0]);
-    Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + hi, wq[1]);
-    Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + lo, wk[0]);
-    Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + hi, wk[1]);
-    // Pair index of this unit's first pair within the head.
-    const int j0 = INTERLEAVED ? uh * 8 : lo;
-    float c[8], s[8];
-    Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0, c);
-    Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0, s);
-
-    // Unpack to 16 values each: x[p][e] is element e of half p.
-    float xq[2][8], xk[2][8];
+  for (int p = 0; p < 2; ++p) {
+    unpack16<IO>(qa[p], xq[p]);
+    unpack16<IO>(ka[p], xk[p]);
+  }
+  float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xq[p][2 * j] = to_f32(IO{uint16_t(qa[i][p][j] & 0xffffu)});
-        xq[p][2 * j + 1] = to_f32(IO{uint16_t(qa[i][p][j] >> 16)});
-        xk[p][2 * j] = to_f32(IO{uint16_t(ka[i][p][j] & 0xffffu)});
-        xk[p][2 * j + 1] = to_f32(IO{uint16_t(ka[i][p][j] >> 16)});
-      }
-    // Norm: (x * r) * w rounded to the io type, as _rms does.
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        xq[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xq[p][e], rq), wq[p][e]));
-        xk[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xk[p][e], rk), wk[p][e]));
-      }
-    // Rotate pair t (t = 0..7) and write back into the same slots.
-    float oq[2][8], ok[2][8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      // Interleaved: pair t is elements (2t, 2t+1) of the 16-element span,
-      // i.e. half t/4, elements 2(t%4) and 2(t%4)+1. Split-half: element t of
-      // half 0 against element t of half 1.
-      const int p_lo = INTERLEAVED ? t / 4 : 0, e_lo = INTERLEAVED ? 2 * (t % 4) : t;
-      const int p_hi = INTERLEAVED ? t / 4 : 1, e_hi = INTERLEAVED ? 2 * (t % 4) + 1 : t;
-      const float ql = xq[p_lo][e_lo], qh = xq[p_hi][e_hi];
-      const float kl = xk[p_lo][e_lo], kh = xk[p_hi][e_hi];
-      oq[p_lo][e_lo] = __fsub_rn(__fmul_rn(ql, c[t]), __fmul_rn(qh, s[t]));
-      oq[p_hi][e_hi] = __fadd_rn(__fmul_rn(ql, s[t]), __fmul_rn(qh, c[t]));
-      ok[p_lo][e_lo] = __fsub_rn(__fmul_rn(kl, c[t]), __fmul_rn(kh, s[t]));
-      ok[p_hi][e_hi] = __fadd_rn(__fmul_rn(kl, s[t]), __fmul_rn(kh, c[t]));
+    for (int e = 0; e < 8; ++e) {
+      sq += xq[p][e] * xq[p][e];
+      sk += xk[p][e] * xk[p][e];
     }
-    u32x4 pq[2], pk[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+  for (int off = 32; off > 0; off >>= 1) {
+    sq += __shfl_xor(sq, off, 64);
+    sk += __shfl_xor(sk, off, 64);
+  }
+  const int wave = threadIdx.x >> 6, n_waves = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) { red[0][wave] = sq; red[1][wave] = sk; }
+  __syncthreads();
+  if (!active) return;
+  float tq = 0.f, tk = 0.f;
+  for (int w = 0; w < n_waves; ++w) { tq += red[0][w]; tk += red[1][w]; }
+  const float HD = float(a.H * a.D);
+  const float rq = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tq, HD) + a.eps));
+  const float rk = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tk, HD) + a.eps));
+
+  // ---- norm (rounded to io, as _rms does), then rotation ------------------
+  float fwq[2][8], fwk[2][8], c[8], s[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pq[p][j] = pack2<IO>(oq[p][2 * j], oq[p][2 * j + 1]);
-        pk[p][j] = pack2<IO>(ok[p][2 * j], ok[p][2 * j + 1]);
-      }
-    const int64_t obase = (int64_t(token) * a.H + h) * a.D;
-    *reinterpret_cast<u32x4*>(a.q_out + obase + lo) = pq[0];
-    *reinterpret_cast<u32x4*>(a.q_out + obase + hi) = pq[1];
-    *reinterpret_cast<u32x4*>(a.k_out + obase + lo) = pk[0];
-    *reinterpret_cast<u32x4*>(a.k_out + obase + hi) = pk[1];
-    if (APPEND) {
-      const int64_t cbase = b * a.c_sb + (a.start + l) * a.c_ss + h * a.c_sh;
-      *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = pk[0];
-      *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = pk[1];
-      const uint16_t* vp = a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
-      *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = *reinterpret_cast<const u32x4*>(vp + lo);
-      *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = *reinterpret_cast<const u32x4*>(vp + hi);
+  for (int p = 0; p < 2; ++p) {
+    Vec8<W>::unpack(wq[p], fwq[p]);
+    Vec8<W>::unpack(wk[p], fwk[p]);
+  }
+  Vec8<TB>::unpack(cr, c);
+  Vec8<TB>::unpack(sr, s);
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xq[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xq[p][e], rq), fwq[p][e]));
+      xk[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xk[p][e], rk), fwk[p][e]));
     }
+  float oq[2][8], ok[2][8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    // Interleaved: pair t is elements (2t, 2t+1) of the 16-element span, i.e.
+    // half t/4, elements 2(t%4) and 2(t%4)+1. Split-half: element t of half 0
+    // against element t of half 1.
+    const int p_lo = INTERLEAVED ? t / 4 : 0, e_lo = INTERLEAVED ? 2 * (t % 4) : t;
+    const int p_hi = INTERLEAVED ? t / 4 : 1, e_hi = INTERLEAVED ? 2 * (t % 4) + 1 : t;
+    const float ql = xq[p_lo][e_lo], qh = xq[p_hi][e_hi];
+    const float kl = xk[p_lo][e_lo], kh = xk[p_hi][e_hi];
+    oq[p_lo][e_lo] = __fsub_rn(__fmul_rn(ql, c[t]), __fmul_rn(qh, s[t]));
+    oq[p_hi][e_hi] = __fadd_rn(__fmul_rn(ql, s[t]), __fmul_rn(qh, c[t]));
+    ok[p_lo][e_lo] = __fsub_rn(__fmul_rn(kl, c[t]), __fmul_rn(kh, s[t]));
+    ok[p_hi][e_hi] = __fadd_rn(__fmul_rn(kl, s[t]), __fmul_rn(kh, c[t]));
+  }
+  u32x4 pq[2], pk[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pq[p][j] = pack2<IO>(oq[p][2 * j], oq[p][2 * j + 1]);
+      pk[p][j] = pack2<IO>(ok[p][2 * j], ok[p][2 * j + 1]);
+    }
+  const int64_t obase = (int64_t(token) * a.H + h) * a.D;
+  *reinterpret_cast<u32x4*>(a.q_out + obase + lo) = pq[0];
+  *reinterpret_cast<u32x4*>(a.q_out + obase + hi) = pq[1];
+  *reinterpret_cast<u32x4*>(a.k_out + obase + lo) = pk[0];
+  *reinterpret_cast<u32x4*>(a.k_out + obase + hi) = pk[1];
+  if (APPEND) {
+    const int64_t cbase = b * a.c_sb + (a.start + l) * a.c_ss + h * a.c_sh;
+    *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = pk[0];
+    *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = pk[1];
+    *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = va[0];
+    *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = va[1];
   }
 }
 
 template <typename IO, typename W, typename TB, bool APPEND>
-hipError_t launch3(const RopeArgs& a, int tokens, bool interleaved, hipStream_t st) {
+hipError_t launch3(const RopeArgs& a, int tokens, int threads, bool interleaved,
+                   hipStream_t st) {
   if (interleaved)
     hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, true, APPEND>), dim3(tokens),
-                       dim3(kThreads), 0, st, a);
+                       dim3(threads), 0, st, a);
   else
     hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, false, APPEND>), dim3(tokens),
-                       dim3(kThreads), 0, st, a);
+                       dim3(threads), 0, st, a);
   return hipGetLastError();
 }
 
 template <typename IO, typename W, bool APPEND>
-hipError_t launch2(const RopeArgs& a, int tokens, int tdt, bool il, hipStream_t st) {
+hipError_t launch2(const RopeArgs& a, int tokens, int threads, int tdt, bool il,
+                   hipStream_t st) {
   switch (tdt) {
-    case DX_BF16: return launch3<IO, W, bf16_t, APPEND>(a, tokens, il, st);
-    case DX_F16: return launch3<IO, W, f16_t, APPEND>(a, tokens, il, st);
-    default: return launch3<IO, W, float, APPEND>(a, tokens, il, st);
+    case DX_BF16: return launch3<IO, W, bf16_t, APPEND>(a, tokens, threads, il, st);
+    case DX_F16: return launch3<IO, W, f16_t, APPEND>(a, tokens, threads, il, st);
+    default: return launch3<IO, W, float, APPEND>(a, tokens, threads, il, st);
   }
 }
 
 template <typename IO, bool APPEND>
-hipError_t launch1(const RopeArgs& a, int tokens, int wdt, int tdt, bool il, hipStream_t st) {
+hipError_t launch1(const RopeArgs& a, int tokens, int threads, int wdt, int tdt, bool il,
+                   hipStream_t st) {
   switch (wdt) {
-    case DX_BF16: return launch2<IO, bf16_t, APPEND>(a, tokens, tdt, il, st);
-    case DX_F16: return launch2<IO, f16_t, APPEND>(a, tokens, tdt, il, st);
-    default: return launch2<IO, float, APPEND>(a, tokens, tdt, il, st);
+    case DX_BF16: return launch2<IO, bf16_t, APPEND>(a, tokens, threads, tdt, il, st);
+    case DX_F16: return launch2<IO, f16_t, APPEND>(a, tokens, threads, tdt, il, st);
+    default: return launch2<IO, float, APPEND>(a, tokens, threads, tdt, il, st);
   }
 }
 
@@ -257,9 +263,8 @@ int check_common(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
   DX_CHECK_ARG(B >= 0 && L >= 0 && H > 0 && D > 0, "qk_norm_rope: bad shape");
   DX_CHECK_ARG(D % 16 == 0, "qk_norm_rope: head_dim %lld must be a multiple of 16",
                (long long)D);
-  DX_CHECK_ARG(H * D <= int64_t(kThreads) * kMaxUnits * 16,
-               "qk_norm_rope: H*D = %lld exceeds %d", (long long)(H * D),
-               kThreads * kMaxUnits * 16);
+  DX_CHECK_ARG(H * D <= int64_t(kMaxThreads) * 16, "qk_norm_rope: H*D = %lld exceeds %d",
+               (long long)(H * D), kMaxThreads * 16);
   DX_CHECK_ARG(B * L < (int64_t(1) << 31), "qk_norm_rope: too many tokens");
   DX_CHECK_ARG(q && k && qw && kw && cos && sin && q_out && k_out,
                "qk_norm_rope: null pointer");
@@ -269,10 +274,9 @@ int check_common(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
   DX_CHECK_ARG(q_sb % 8 == 0 && q_sl % 8 == 0 && q_sh % 8 == 0 && k_sb % 8 == 0 &&
                    k_sl % 8 == 0 && k_sh % 8 == 0,
                "qk_norm_rope: q/k strides must be multiples of 8 elements");
-  const int64_t tb = (tdt == DX_F32) ? 4 : 8;  // elements per 16 bytes... for alignment
-  DX_CHECK_ARG(cos_sl % tb == 0 && sin_sl % tb == 0,
+  const int64_t per16 = (tdt == DX_F32) ? 4 : 8;  // table elements per 16 bytes
+  DX_CHECK_ARG(cos_sl % per16 == 0 && sin_sl % per16 == 0,
                "qk_norm_rope: cos/sin row strides must keep rows 16-byte aligned");
-  (void)tb;
   return DX_OK;
 }
 
@@ -321,13 +325,15 @@ static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
   a.L = int(L); a.H = int(H); a.D = int(D); a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int tokens = int(B * L);
+  const int units = int(H * D / 16);
+  const int threads = (units + 63) / 64 * 64;
   hipError_t e;
   if (io_dtype == DX_BF16)
-    e = append ? launch1<bf16_t, true>(a, tokens, wdt, tdt, interleaved != 0, st)
-               : launch1<bf16_t, false>(a, tokens, wdt, tdt, interleaved != 0, st);
+    e = append ? launch1<bf16_t, true>(a, tokens, threads, wdt, tdt, interleaved != 0, st)
+               : launch1<bf16_t, false>(a, tokens, threads, wdt, tdt, interleaved != 0, st);
   else
-    e = append ? launch1<f16_t, true>(a, tokens, wdt, tdt, interleaved != 0, st)
-               : launch1<f16_t, false>(a, tokens, wdt, tdt, interleaved != 0, st);
+    e = append ? launch1<f16_t, true>(a, tokens, threads, wdt, tdt, interleaved != 0, st)
+               : launch1<f16_t, false>(a, tokens, threads, wdt, tdt, interleaved != 0, st);
   if (e != hipSuccess) {
     set_error("qk_norm_rope: launch failed: %s", hipGetErrorString(e));
     return DX_ELAUNCH;

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -79,7 +79,8 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         ctypes.POINTER(ctypes.c_int64), _p, _i, _l,
         _i, _f,
         _p, _l, _p]),
-    "dx_attention_workspace_bytes": (_l, [_l, _l, _l, _l, _l, _l]),
+    "dx_attention_workspace_bytes": (_l, [_l, _l, _l, _l, _l, _l,
+                                          ctypes.POINTER(ctypes.c_int64)]),
 }
 
 _lock = threading.Lock()

@@ -35,8 +35,7 @@ def _accepts(q, k, v, *args, **kwargs) -> bool:
     return (q.is_cuda and q.dtype in MATRIX_DTYPES and q.dim() == 4
             and k.dtype == q.dtype and v.dtype == q.dtype
             and k.shape == v.shape and k.dim() == 4
-            and q.shape[-1] in (64, 128) and k.shape[-1] == q.shape[-1]
-            and k.shape[1] == q.shape[1])
+            and q.shape[-1] in (64, 128) and k.shape[-1] == q.shape[-1])
 
 
 def _starts(block_boundaries, q_len: int, device: torch.device):
@@ -94,7 +93,10 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
     out = torch.empty((b, q_len, heads, dim), device=q.device, dtype=q.dtype)
     starts, starts_dt, n_blocks = _starts(block_boundaries, q_len, q.device)
     lib = _lib.load()
-    ws_bytes = lib.dx_attention_workspace_bytes(b, q_len, q_len, heads, dim, max_cache)
+    arr = None
+    if cache_lens is not None:
+        arr = (_lib.ctypes.c_int64 * b)(*[int(x) for x in cache_lens])
+    ws_bytes = lib.dx_attention_workspace_bytes(b, q_len, q_len, heads, dim, int(cache_len), arr)
     if ws_bytes < 0:
         _lib.check(-ws_bytes, "attention workspace")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
@@ -108,7 +110,6 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
     if cache_lens is None:
         rc = lib.dx_blockwise_causal_attention(*common, int(cache_len), *tail)
     else:
-        arr = (_lib.ctypes.c_int64 * b)(*[int(x) for x in cache_lens])
         rc = lib.dx_blockwise_causal_attention_varlen(*common, arr, *tail)
     _lib.check(rc, "blockwise_causal_attention")
     return out

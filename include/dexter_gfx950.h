@@ -59,7 +59,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 1
+#define DX_ABI_VERSION 2
 
 /*
  * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.
@@ -165,11 +165,13 @@ int dx_blockwise_causal_attention_varlen(
 /*
  * Workspace bytes the attention entry points need for this shape on the
  * current device (split-KV partial results); 0 when the launch does not split.
- * max_cache_len is cache_len, or the largest cache_lens[b] for varlen.
+ * Pass cache_len and cache_lens = NULL for dx_blockwise_causal_attention, or
+ * the same cache_lens array (cache_len ignored) for the varlen entry point.
  * Returns a negative DX_E* code on a bad shape.
  */
 int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
-                                     int64_t D, int64_t max_cache_len);
+                                     int64_t D, int64_t cache_len,
+                                     const int64_t* cache_lens);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,7 @@ from dexter_amd.bench.workloads import CONFIGS, block_tensor, make_inputs
 from oracle import attention as oatt
 from oracle import rope as orope
 
-from _util import assert_parity
+from _util import assert_parity, assert_parity_scaled
 
 pytestmark = pytest.mark.gpu
 
@@ -140,4 +140,6 @@ def test_c4_ragged_batch(device, built_lib):
         ref = oatt.blockwise_causal_attention(inp.q[i:i + 1], kq[i:i + 1], vq[i:i + 1],
                                               cache[:, i:i + 1], c, torch.tensor(cfg.block_starts),
                                               None, keep_fp32=True)
-        assert_parity(got[i:i + 1], ref, what=f"C4 seq {i} (cache {c})")
+        # x20 outliers push |out| to tens: the bf16 output alone rounds by
+        # up to 2^-9 |out|, so the max-abs bar scales with |ref| above 1.
+        assert_parity_scaled(got[i:i + 1], ref, what=f"C4 seq {i} (cache {c})")
