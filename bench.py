@@ -62,16 +62,20 @@ def _per_layer_inputs(inp, device, layers: int, cache_len: int):
 
     import dexter_amd.ops as ops
 
+    from dexter_amd.models.kv_cache import head_major_cache
+
     cfg = inp.cfg
     c = cache_len
     q, k, v = inp.q.to(device), inp.k.to(device), inp.v.to(device)
     qw, kw = inp.q_weight.to(device), inp.k_weight.to(device)
     cos, sin = inp.cos.to(device), inp.sin.to(device)
-    base = torch.zeros(2, cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim, dtype=cfg.dtype,
-                       device=device)
     _, kr = ops.qk_norm_rope(q[:, :c], k[:, :c], qw, kw, cos[:c], sin[:c])
-    ops.kv_cache_append(base, kr, v[:, :c], 0)
-    caches = [base.clone() for _ in range(layers)]
+    caches = []
+    for _ in range(layers):  # the model's per-layer caches (head-major storage)
+        cache = head_major_cache(cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim, device,
+                                 cfg.dtype)
+        ops.kv_cache_append(cache, kr, v[:, :c], 0)
+        caches.append(cache)
     chunk = [tuple(t[:, c:].clone() for t in (q, k, v)) for _ in range(layers)]
     tables = (cos[c:].contiguous(), sin[c:].contiguous())
     torch.cuda.synchronize()
@@ -171,6 +175,7 @@ def run_config(name: str, device, reps: int) -> dict:
     import dexter_amd.ops as ops
     from dexter_amd.bench import harness
     from dexter_amd.bench.workloads import CONFIGS, block_tensor, make_inputs
+    from dexter_amd.models.kv_cache import head_major_cache
 
     cfg = CONFIGS[name]
     inp = make_inputs(cfg)
@@ -178,13 +183,14 @@ def run_config(name: str, device, reps: int) -> dict:
     if name == "C4":
         lens = list(cfg.cache_lens)
         b, h, d = cfg.batch, cfg.heads, cfg.head_dim
-        cache = torch.zeros(2, b, max(lens), h, d, dtype=cfg.dtype)
+        cache = head_major_cache(b, max(lens), h, d, device, cfg.dtype)
         kq = torch.zeros(b, cfg.q_len, h, d, dtype=cfg.dtype)
         vq = torch.zeros_like(kq)
         for i, c in enumerate(lens):
-            cache[0, i, :c], cache[1, i, :c] = inp.k[i, :c], inp.v[i, :c]
+            cache[0, i, :c] = inp.k[i, :c].to(device)
+            cache[1, i, :c] = inp.v[i, :c].to(device)
             kq[i], vq[i] = inp.k[i, c:c + cfg.q_len], inp.v[i, c:c + cfg.q_len]
-        q, kq, vq, cache = (t.to(device) for t in (inp.q, kq, vq, cache))
+        q, kq, vq = (t.to(device) for t in (inp.q, kq, vq))
 
         def call():
             ops.blockwise_causal_attention_varlen(q, kq, vq, kv_cache=cache, cache_lens=lens,
@@ -197,8 +203,8 @@ def run_config(name: str, device, reps: int) -> dict:
         qr, kr = ops.qk_norm_rope(q, k, qw, kw, cos, sin)
         cache = None
         if c:
-            cache = torch.zeros(2, cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim,
-                                dtype=cfg.dtype, device=device)
+            cache = head_major_cache(cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim, device,
+                                     cfg.dtype)
             ops.kv_cache_append(cache, kr[:, :c], v[:, :c], 0)
         qc, kc, vc = qr[:, c:].contiguous(), kr[:, c:].contiguous(), v[:, c:].contiguous()
         del q, k, qr, kr

@@ -17,8 +17,9 @@
 // registers. Because the K index of an MFMA may be assigned to (lane group,
 // element) slots in any order as long as A and B agree, the eight keys a lane
 // contributes per 16-key step are {4g..4g+3, 8+4g..8+4g+3} (g = lane / 32),
-// and V^T is staged in LDS with each 16-key group stored in the order
-// [0-3, 8-11, 4-7, 12-15] so each A operand is one 16-byte LDS read.
+// exactly the keys its accumulator registers hold; the matching V^T operand
+// is read from the row-major V tile with two gfx950 transposing LDS reads
+// (ds_read_b64_tr_b16), so V is never transposed in registers.
 //
 // Softmax. Exponentials are v_exp_f32 on fma(score, scale*log2e, -ref).
 // The reference max is refreshed lazily: only when some lane's max grows by
@@ -74,8 +75,8 @@ struct AttnArgs {
   const uint16_t* v; int64_t v_sb, v_sl, v_sh;
   const uint16_t* ck; const uint16_t* cv; int64_t c_sb, c_ss, c_sh;
   uint16_t* out; int64_t o_sb, o_sl, o_sh;
-  float* ws_o;   // [partials][kBM][D] unnormalised accumulators
-  float* ws_ml;  // [partials][kBM][2]  (exponent reference in log2 units, sum)
+  uint16_t* ws_o;  // [partials][kBM][D] f16 normalised partial outputs acc / l
+  float* ws_ml;    // [partials][kBM][2] (exponent reference in log2 units, sum l)
   const void* starts; int starts_i64; int n_blocks;
   int B, H, Lq, Lk;
   int causal;
@@ -158,6 +159,37 @@ template <int D> struct Lds {
                 "a stream's region must hold the (max, sum, acc) hand-over");
 };
 
+// Where a workgroup reads its keys and values: raw buffer descriptors over
+// the cached rows and over the new rows of one (batch, head), each bounded to
+// the rows the workgroup may see. Offsets are 32-bit bytes (the host checks
+// they fit); a row past a descriptor's bound reads as zeros without touching
+// memory, so rows at or past kv_max (and past the cache's end) are
+// zero-filled without a branch.
+//
+// Key tiles never straddle the two sources: tiles [0, n_ct) cover the cache
+// (the last one possibly partial), tiles [n_ct, ...) the new keys from key
+// cache_len on. Each tile then has one descriptor and one row stride,
+// selected with scalar instructions, and one load path.
+struct KvSrc {
+  __amdgpu_buffer_rsrc_t kc, vc, kn, vn;
+  __amdgpu_buffer_rsrc_t none;  // zero records: every lane reads zeros
+  int c_ss2, k_sl2, v_sl2;  // row strides in bytes
+  int n_ct;                 // cache tiles: ceil(cache_len / kBN)
+};
+
+constexpr int kBufWord3 = 0x00020000;  // gfx9-family raw buffer descriptor word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base, int rows,
+                                                           int row_bytes, int D) {
+  const int bytes = rows > 0 ? (rows - 1) * row_bytes + D * 2 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, bytes,
+                                           kBufWord3);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // One K tile and one V tile of a workgroup's share, staged in registers
 // between the global load and the LDS store. Thread x moves 16-byte chunks
 // x, x + 256, ... of each tile: 16 consecutive threads cover one 256-byte
@@ -168,27 +200,27 @@ struct TileRegs {
   static constexpr int CPR = D / 8;        // 16-byte chunks per key row
   static constexpr int CH = kBN * CPR;     // chunks per tile
   static constexpr int CPT = CH / NT;      // chunks per thread
+  static constexpr int RPI = NT / CPR;     // rows between a thread's consecutive chunks
   static_assert(CH % NT == 0, "tile must split evenly over the threads");
   u32x4 kr[CPT], vr[CPT];
 
-  // Rows at or past kv_max are zero-filled, never read.
-  __device__ __forceinline__ void load(int tid, const uint16_t* kc, const uint16_t* kn,
-                                       const uint16_t* vc, const uint16_t* vn,
-                                       int64_t c_ss, int64_t k_sl, int64_t v_sl,
-                                       int cache_len, int kv_max, int j0) {
+  // Tile t (uniform). ``live`` false loads nothing (a descriptor of zero
+  // records: all lanes read zeros) but keeps one straight-line path, so the
+  // compiler's wait counts for earlier loads stay exact.
+  __device__ __forceinline__ void load(int tid, const KvSrc& src, int t, bool live) {
+    const int r0 = tid / CPR, colb = (tid % CPR) * 16;
+    const bool in_cache = t < src.n_ct;
+    __amdgpu_buffer_rsrc_t rk = in_cache ? src.kc : src.kn;
+    __amdgpu_buffer_rsrc_t rv = in_cache ? src.vc : src.vn;
+    if (!live) rk = rv = src.none;
+    const int sk = in_cache ? src.c_ss2 : src.k_sl2;
+    const int sv = in_cache ? src.c_ss2 : src.v_sl2;
+    const int row = (in_cache ? t : t - src.n_ct) * kBN + r0;
+    const int ok = row * sk + colb, ov = row * sv + colb;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * NT;
-      const int j = j0 + c / CPR, col = (c % CPR) * 8;
-      kr[i] = u32x4{0, 0, 0, 0};
-      vr[i] = u32x4{0, 0, 0, 0};
-      if (j < kv_max) {
-        const bool cached = j < cache_len;
-        const uint16_t* pk = cached ? kc + j * c_ss : kn + (j - cache_len) * k_sl;
-        const uint16_t* pv = cached ? vc + j * c_ss : vn + (j - cache_len) * v_sl;
-        kr[i] = *reinterpret_cast<const u32x4*>(pk + col);
-        vr[i] = *reinterpret_cast<const u32x4*>(pv + col);
-      }
+      kr[i] = buf_load16(rk, ok + i * RPI * sk);
+      vr[i] = buf_load16(rv, ov + i * RPI * sv);
     }
   }
 
@@ -279,11 +311,13 @@ struct Softmax {
 };
 
 // One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.
-// ``full`` = every key of the tile is visible to every query of the workgroup.
+// ``masked``: some key of the tile is invisible to some query of the
+// workgroup (a straddling tile; workgroup-uniform). Unmasked tiles do no
+// per-key visibility work.
 template <int D, typename T>
 __device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs,
                                           const u32x4 (&qr)[D / 16], f32x16 (&acc)[D / 32],
-                                          Softmax& sm, float c, int j0, int my_end, bool full,
+                                          Softmax& sm, float c, int lim_rel, bool masked,
                                           int lane) {
   constexpr int KS = D / 16, DT = D / 32;
   const int n = lane & 31, g = lane >> 5;
@@ -296,49 +330,58 @@ __device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs
     for (int ks = 0; ks < KS; ++ks)
       s[kt] = Mfma<T>::run(*reinterpret_cast<const u32x4*>(kp + 16 * ks), qr[ks], s[kt]);
   }
+  // Key of register r of half kt: row 32 kt + 8 (r / 4) + 4 g + r % 4 of the
+  // tile, visible iff that row is below lim_rel (rows past the tile's valid
+  // keys or past this query's visible end are not).
+  const int lim = lim_rel - 4 * g;
+  if (masked) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (32 * kt + 8 * (r / 4) + (r % 4) >= lim) s[kt][r] = -INFINITY;
+  }
   // Row max over the visible scores (raw units; c >= 0 keeps the order).
   float tmax = -INFINITY;
-  if (full) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
-  } else {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = j0 + 32 * kt + 8 * (r / 4) + 4 * g + (r % 4);
-        tmax = fmaxf(tmax, key < my_end ? s[kt][r] : -INFINITY);
-      }
-  }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-  const float m_new = fmaxf(sm.m, tmax);
-  // Lazy rescale (wave-uniform branch). First visible tile: m = -inf, always.
-  const bool grow = (m_new - sm.m) * c > 8.0f;
-  if (__any(grow)) {
-    const float corr = sm.m == -INFINITY ? 0.f : fast_exp2((sm.m - m_new) * c);
-    sm.l *= corr;
-#pragma unroll
-    for (int d = 0; d < DT; ++d) acc[d] *= corr;
-    sm.m = m_new;
-  }
-  // Nothing visible yet: exponent base 0; masked p are set to 0 below.
-  const float mb = sm.m == -INFINITY ? 0.f : sm.m * c;
-  float psum = 0.f;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float p = fast_exp2(__builtin_fmaf(s[kt][r], c, -mb));
-      if (!full) {
-        const int key = j0 + 32 * kt + 8 * (r / 4) + 4 * g + (r % 4);
-        p = key < my_end ? p : 0.f;
-      }
-      s[kt][r] = p;
-      psum += p;
+    for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const float m_new = fmaxf(sm.m, tmax);
+  // Lazy rescale (wave-uniform branch): only when some lane's max grew by
+  // more than 2^8. Before anything is accumulated (m = -inf on every lane)
+  // there is nothing to scale: just take the new reference.
+  const bool grow = (m_new - sm.m) * c > 8.0f;
+  if (__any(grow)) {
+    if (!__all(sm.m == -INFINITY)) {
+      const float corr = sm.m == -INFINITY ? 0.f : fast_exp2((sm.m - m_new) * c);
+      sm.l *= corr;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) acc[d] *= corr;
     }
-  sm.l += psum;
+    sm.m = m_new;
+  }
+  // Nothing visible yet: exponent base 0.
+  const float mb = sm.m == -INFINITY ? 0.f : sm.m * c;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[kt][r] = fast_exp2(__builtin_fmaf(s[kt][r], c, -mb));
+  // exp2(-inf * c) is 0 for c > 0 but NaN for c == 0: zero masked p explicitly.
+  if (masked) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (32 * kt + 8 * (r / 4) + (r % 4) >= lim) s[kt][r] = 0.f;
+  }
+  float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[r % 4] += s[kt][r];
+  sm.l += (part[0] + part[1]) + (part[2] + part[3]);
   // O^T += V^T P^T, 16 keys per MFMA (key step u = 2 kt + hf). The A
   // operand of lane (n, g) is head_dim column 32 d + n at keys
   // 16u + {4g..4g+3, 8+4g..8+4g+3}, gathered from the row-major V tile by two
@@ -373,9 +416,14 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   const Coord it = locate(a, blockIdx.x, false, 0);
   const int b = it.b, h = it.h;
   // NS streams of four waves; stream s takes every NS-th tile of the range.
-  const int stream = NS == 1 ? 0 : int(threadIdx.x) / (64 * kNW);
-  const int ltid = int(threadIdx.x) - stream * 64 * kNW;
-  const int wave = ltid >> 6, lane = ltid & 63;
+  // Wave and stream indices are read through readfirstlane so the compiler
+  // treats them as wave-uniform: branches on them become scalar branches
+  // instead of exec-masked regions (which would serialise the loads issued
+  // on either side).
+  const int wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int stream = NS == 1 ? 0 : wid / kNW;
+  const int wave = wid - stream * kNW, lane = int(threadIdx.x) & 63;
+  const int ltid = wave * 64 + lane;
   const int g = lane >> 5, n = lane & 31;
   const int q0 = it.qtile * kBM;
   const int qi = q0 + wave * 32 + n;
@@ -390,35 +438,82 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   const int kv_min = cache_len + visible_end(a, q0);
   const int kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
 
-  const int n_tiles = (kv_max + kBN - 1) / kBN;
+  const int n_ct = (cache_len + kBN - 1) / kBN;
+  const int n_tiles = n_ct + (kv_max - cache_len + kBN - 1) / kBN;
   const int t_begin = int((int64_t(it.split) * n_tiles) / it.n_splits);
   const int t_end = int((int64_t(it.split + 1) * n_tiles) / it.n_splits);
   const int iters = (t_end - t_begin + NS - 1) / NS;  // barrier rounds, equal for all streams
 
-  const uint16_t* kc = a.ck + b * a.c_sb + h * a.c_sh;
-  const uint16_t* vc = a.cv + b * a.c_sb + h * a.c_sh;
-  const uint16_t* kn = a.k + b * a.k_sb + h * a.k_sh;
-  const uint16_t* vn = a.v + b * a.v_sb + h * a.v_sh;
+  KvSrc src;
+  src.c_ss2 = int(a.c_ss) * 2;
+  src.k_sl2 = int(a.k_sl) * 2;
+  src.v_sl2 = int(a.v_sl) * 2;
+  src.n_ct = n_ct;
+  {
+    const int rows_c = min(cache_len, kv_max), rows_n = kv_max - cache_len;
+    const int64_t coff = b * a.c_sb + h * a.c_sh;
+    src.kc = make_rsrc(a.ck ? a.ck + coff : a.q, rows_c, src.c_ss2, D);
+    src.vc = make_rsrc(a.cv ? a.cv + coff : a.q, rows_c, src.c_ss2, D);
+    src.kn = make_rsrc(a.k + b * a.k_sb + h * a.k_sh, rows_n, src.k_sl2, D);
+    src.vn = make_rsrc(a.v + b * a.v_sb + h * a.v_sh, rows_n, src.v_sl2, D);
+    src.none = make_rsrc(a.q, 0, 0, D);
+  }
 
-  // Request this stream's first tile before anything waits on memory.
+  // Q^T operand: lane holds query n, head_dim [16s + 8g, 16s + 8g + 8) per
+  // k-step s. With two streams, wave w of each stream needs the same 32
+  // queries: each stream fetches half of the k-steps and the halves are
+  // swapped through LDS, so Q crosses the memory system once per workgroup.
+  // Q loads go out first (they are needed first), then this stream's first
+  // tile.
+  // Register indices must stay compile-time constants, so the stream choice
+  // is a (wave-uniform) branch around fixed-index loops.
+  constexpr int KQ = KS / NS;  // k-steps this stream fetches
+  u32x4 qr[KS];
+  // Rows past the end load the last row (an address in bounds, no branch)
+  // and are zeroed once the tile loads are out.
+  const uint16_t* qp =
+      a.q + b * a.q_sb + int64_t(min(qi, a.Lq - 1)) * a.q_sl + h * a.q_sh + 8 * g;
+  if (stream == 0) {
+#pragma unroll
+    for (int s = 0; s < KQ; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+  } else {
+#pragma unroll
+    for (int s = KQ; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+  }
+
   TileRegs<D> regs;
   const int t_first = t_begin + stream;
-  if (t_first < t_end)
-    regs.load(ltid, kc, kn, vc, vn, a.c_ss, a.k_sl, a.v_sl, cache_len, kv_max, t_first * kBN);
+  regs.load(ltid, src, t_first, t_first < t_end);
 
   // Visible-key end of this lane's query (per-key masking of straddling tiles).
   const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
 
-  // Q^T operand: lane holds query n, head_dim [16s + 8g, 16s + 8g + 8) per k-step s.
-  u32x4 qr[KS];
+  if (NS == 2) {
+    // Exchange area: the first tile buffer of stream 1 (not yet written).
+    static_assert(kBM * Lds<D>::kPitch <= Lds<D>::stage, "Q exchange must fit one stage");
+    uint16_t* qx = smem + 2 * Lds<D>::stage + (wave * 32 + n) * Lds<D>::kPitch + 8 * g;
+    if (stream == 0) {
+#pragma unroll
+      for (int s = 0; s < KQ; ++s) *reinterpret_cast<u32x4*>(qx + 16 * s) = qr[s];
+    } else {
+#pragma unroll
+      for (int s = KQ; s < KS; ++s) *reinterpret_cast<u32x4*>(qx + 16 * s) = qr[s];
+    }
+    __syncthreads();
+    if (stream == 0) {
+#pragma unroll
+      for (int s = KQ; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qx + 16 * s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KQ; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qx + 16 * s);
+    }
+    __syncthreads();  // exchange read before stream 1's first tile overwrites it
+  }
   {
-    const uint16_t* qp = a.q + b * a.q_sb + int64_t(qi) * a.q_sl + h * a.q_sh;
+    const uint32_t qmask = qvalid ? ~0u : 0u;
     const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      qr[s] = qvalid ? *reinterpret_cast<const u32x4*>(qp + 16 * s + 8 * g) : u32x4{0, 0, 0, 0};
-      qr[s] ^= flip;
-    }
+    for (int s = 0; s < KS; ++s) qr[s] = (qr[s] & qmask) ^ flip;
   }
 
   f32x16 acc[DT];
@@ -436,12 +531,17 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     uint16_t* const st = region + (i & 1) * Lds<D>::stage;
     if (t < t_end) regs.store(ltid, st, st + Lds<D>::kElems);
     __syncthreads();
-    if (t + NS < t_end)
-      regs.load(ltid, kc, kn, vc, vn, a.c_ss, a.k_sl, a.v_sl, cache_len, kv_max,
-                (t + NS) * kBN);
-    if (wave_active && t < t_end)
-      tile_step<D, T>(st, st + Lds<D>::kElems, qr, acc, sm, c, t * kBN, my_end,
-                      (t + 1) * kBN <= kv_min, lane);
+    if (t + NS < t_end) regs.load(ltid, src, t + NS, true);
+    if (wave_active && t < t_end) {
+      // Cache tiles: every query sees every cached key; only the partial
+      // last one masks (its rows past cache_len). New-key tiles mask where
+      // they reach past kv_min.
+      const bool in_cache = t < n_ct;
+      const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
+      const int lim_rel = in_cache ? cache_len - j0 : my_end - j0;
+      const bool masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
+      tile_step<D, T>(st, st + Lds<D>::kElems, qr, acc, sm, c, lim_rel, masked, lane);
+    }
   }
 
   // The exponent reference of acc and l, in log2 units.
@@ -491,19 +591,27 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
         *reinterpret_cast<u32x2*>(op + dim) = w;
       }
   } else {
+    // Split-KV partial: the normalised output acc / l of this key range in
+    // f16 (|value| <= max |v|, 11-bit mantissa) plus (reference, l) in fp32;
+    // the merge re-weights by l. No visible key: o = 0, reference -inf.
     const int64_t pidx = it.pbase + it.split;
     const int row = wave * 32 + n;
-    float* po = a.ws_o + (pidx * kBM + row) * D;
+    const bool any = l_tot > 0.f;
+    const float inv = any ? 1.0f / l_tot : 0.f;
+    uint16_t* po = a.ws_o + (pidx * kBM + row) * D;
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int dim = 32 * d + 8 * r4 + 4 * g;
-        *reinterpret_cast<f32x4*>(po + dim) =
-            f32x4{acc[d][4 * r4], acc[d][4 * r4 + 1], acc[d][4 * r4 + 2], acc[d][4 * r4 + 3]};
+        u32x2 w;
+        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
+        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(po + dim) = w;
       }
     if (g == 0)
-      *reinterpret_cast<float2*>(a.ws_ml + (pidx * kBM + row) * 2) = make_float2(mref, l_tot);
+      *reinterpret_cast<float2*>(a.ws_ml + (pidx * kBM + row) * 2) =
+          make_float2(any ? mref : -INFINITY, l_tot);
   }
 }
 
@@ -526,12 +634,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int qi = cd.qtile * kBM + row;
   if (row >= kBM || qi >= a.Lq) return;
   float2 ml[kMaxSplits];
-  f32x4 o[kMaxSplits];
+  u32x2 o[kMaxSplits];
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
     if (s < cd.n_splits) {
       ml[s] = *reinterpret_cast<const float2*>(a.ws_ml + ((cd.pbase + s) * kBM + row) * 2);
-      o[s] = *reinterpret_cast<const f32x4*>(a.ws_o + ((cd.pbase + s) * kBM + row) * D + dim);
+      o[s] = *reinterpret_cast<const u32x2*>(a.ws_o + ((cd.pbase + s) * kBM + row) * D + dim);
     }
   }
   float mmax = -INFINITY;
@@ -544,12 +652,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
     if (s < cd.n_splits) {
-      const float w = fast_exp2(ml[s].x - base);
-      l += w * ml[s].y;
-      acc += w * o[s];
+      // Weight of split s: its exponent offset times its own sum (o_s is normalised).
+      const float w = fast_exp2(ml[s].x - base) * ml[s].y;
+      l += w;
+      acc[0] += w * to_f32(f16_t{uint16_t(o[s][0] & 0xffffu)});
+      acc[1] += w * to_f32(f16_t{uint16_t(o[s][0] >> 16)});
+      acc[2] += w * to_f32(f16_t{uint16_t(o[s][1] & 0xffffu)});
+      acc[3] += w * to_f32(f16_t{uint16_t(o[s][1] >> 16)});
     }
   }
-  const float inv = 1.0f / l;
+  const float inv = 1.0f / l;  // no visible key anywhere: 0 * inf = NaN, as the reference
   uint16_t* op = a.out + cd.b * a.o_sb + int64_t(qi) * a.o_sl + cd.h * a.o_sh + dim;
   u32x2 w2;
   w2[0] = Mfma<T>::pack(acc[0] * inv, acc[1] * inv);
@@ -630,7 +742,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
   const int cus = device_cus();
   const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
   if (!cache_lens) {
-    const int64_t tiles = cdiv(cache_len + Lq, kBN);
+    const int64_t tiles = cdiv(cache_len, kBN) + cdiv(Lq, kBN);
     p.uniform_splits = choose_uniform_splits(B * per_b, tiles, cus, p.streams);
     p.items = B * per_b * p.uniform_splits;
     p.partials = p.uniform_splits > 1 ? p.items : 0;
@@ -646,7 +758,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
     std::vector<int64_t> tiles(B);
     int64_t total = 0;
     for (int i = 0; i < int(B); ++i) {
-      tiles[i] = cdiv(cache_lens[i] + Lq, kBN);
+      tiles[i] = cdiv(cache_lens[i], kBN) + cdiv(Lq, kBN);
       total += tiles[i];
     }
     std::vector<int> splits(B, 1);
@@ -682,7 +794,8 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
     p.comb_blocks = p.comb_base.back();
     p.partials = p.items;
   }
-  p.ws_bytes = p.comb_blocks > 0 ? p.partials * kBM * (D + 2) * int64_t(sizeof(float)) : 0;
+  // f16 partial outputs, then fp32 (reference, sum) pairs.
+  p.ws_bytes = p.comb_blocks > 0 ? p.partials * kBM * (D * 2 + 2 * int64_t(sizeof(float))) : 0;
   return p;
 }
 
@@ -759,6 +872,14 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                    (!cache || (c_plane % 8 == 0 && c_sb % 8 == 0 && c_ss % 8 == 0 &&
                                c_sh % 8 == 0)),
                "attention: strides must be multiples of 8 elements");
+  {
+    // Key/value rows are addressed with 32-bit byte offsets per (batch, head).
+    const int64_t rows = max_cache + Lq;
+    const int64_t stride = std::max({cache ? c_ss : int64_t(0), k_sl, v_sl});
+    DX_CHECK_ARG(rows * stride * 2 < (int64_t(1) << 31),
+                 "attention: %lld rows of stride %lld exceed 32-bit offsets", (long long)rows,
+                 (long long)stride);
+  }
   if (B * Lq == 0) return DX_OK;
   const Plan p = make_plan(B, Lq, H, D, cache_len, cache_lens);
   DX_CHECK_ARG(p.items < (int64_t(1) << 31), "attention: grid too large");
@@ -778,8 +899,8 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.cv = cache ? static_cast<const uint16_t*>(cache) + c_plane : nullptr;
   a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh;
   a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
-  a.ws_o = static_cast<float*>(workspace);
-  a.ws_ml = p.ws_bytes ? a.ws_o + p.partials * kBM * D : nullptr;
+  a.ws_o = static_cast<uint16_t*>(workspace);
+  a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * kBM * D) : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
   a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);
   a.causal = causal != 0;

@@ -139,6 +139,22 @@ def test_split_kv_decode_shape(device, built_lib):
     assert_parity(got, ref)
 
 
+def test_head_major_cache_matches_contiguous_bit_exact(device, built_lib):
+    """KVCache stores [2, B, H, S, D] and hands out the [2, B, S, H, D] view;
+    the kernel reads either layout through its strides, with identical results."""
+    from dexter_amd.models.kv_cache import head_major_cache
+    b, l, h, d, cache_len = 2, 83, 24, 128, 1245
+    q, k, v = (_rand((b, l, h, d), device, seed=s) for s in (43, 44, 45))
+    dense = _rand((2, b, cache_len + l, h, d), device, seed=46)
+    hm = head_major_cache(b, cache_len + l, h, d, device, DT)
+    hm.copy_(dense)
+    assert not hm.is_contiguous() and hm.stride(2) == d
+    a = ops.blockwise_causal_attention(q, k, v, kv_cache=dense, cache_len=cache_len)
+    c = ops.blockwise_causal_attention(q, k, v, kv_cache=hm, cache_len=cache_len)
+    assert torch.equal(a, c)
+    assert_parity(c, _oracle(q, k, v, dense, cache_len, None))
+
+
 def test_rows_before_the_first_block_match_the_reference(device, built_lib):
     """Rows before block_boundaries[0] see only the cache; with no cache they are NaN."""
     b, l, h, d = 1, 40, 2, 64
