@@ -62,7 +62,6 @@ def _per_layer_inputs(inp, device, layers: int, cache_len: int):
 
     import dexter_amd.ops as ops
 
-    from dexter_amd.models.kv_cache import head_major_cache
 
     cfg = inp.cfg
     c = cache_len
@@ -71,9 +70,9 @@ def _per_layer_inputs(inp, device, layers: int, cache_len: int):
     cos, sin = inp.cos.to(device), inp.sin.to(device)
     _, kr = ops.qk_norm_rope(q[:, :c], k[:, :c], qw, kw, cos[:c], sin[:c])
     caches = []
-    for _ in range(layers):  # the model's per-layer caches (head-major storage)
-        cache = head_major_cache(cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim, device,
-                                 cfg.dtype)
+    for _ in range(layers):  # the model's per-layer caches
+        cache = torch.zeros(2, cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim,
+                            device=device, dtype=cfg.dtype)
         ops.kv_cache_append(cache, kr, v[:, :c], 0)
         caches.append(cache)
     chunk = [tuple(t[:, c:].clone() for t in (q, k, v)) for _ in range(layers)]
@@ -154,7 +153,8 @@ def run_headline(args, device):
             "bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
             "frac": achieved / PEAK_HBM_GBPS,
             "traffic": traffic["bytes"] if traffic else None,
-            "kernel": "attn_fwd_kernel<3,128,bf16> + attn_combine_kernel (split-KV), C1",
+            "kernel": ("one attention call at C1 = attn_fwd_kernel<128,bf16_t,2> (split-KV, "
+                       "dual-stream) + attn_combine_kernel<128,bf16_t>"),
             "algorithmic_bytes_per_launch": attn_bytes,
             "launch_us": attn_ms * 1e3,
             "tflops": flops / (attn_ms * 1e-3) / 1e12,
@@ -175,7 +175,6 @@ def run_config(name: str, device, reps: int) -> dict:
     import dexter_amd.ops as ops
     from dexter_amd.bench import harness
     from dexter_amd.bench.workloads import CONFIGS, block_tensor, make_inputs
-    from dexter_amd.models.kv_cache import head_major_cache
 
     cfg = CONFIGS[name]
     inp = make_inputs(cfg)
@@ -183,7 +182,7 @@ def run_config(name: str, device, reps: int) -> dict:
     if name == "C4":
         lens = list(cfg.cache_lens)
         b, h, d = cfg.batch, cfg.heads, cfg.head_dim
-        cache = head_major_cache(b, max(lens), h, d, device, cfg.dtype)
+        cache = torch.zeros(2, b, max(lens), h, d, device=device, dtype=cfg.dtype)
         kq = torch.zeros(b, cfg.q_len, h, d, dtype=cfg.dtype)
         vq = torch.zeros_like(kq)
         for i, c in enumerate(lens):
@@ -203,8 +202,8 @@ def run_config(name: str, device, reps: int) -> dict:
         qr, kr = ops.qk_norm_rope(q, k, qw, kw, cos, sin)
         cache = None
         if c:
-            cache = head_major_cache(cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim, device,
-                                     cfg.dtype)
+            cache = torch.zeros(2, cfg.batch, c + cfg.q_len, cfg.heads, cfg.head_dim,
+                                device=device, dtype=cfg.dtype)
             ops.kv_cache_append(cache, kr[:, :c], v[:, :c], 0)
         qc, kc, vc = qr[:, c:].contiguous(), kr[:, c:].contiguous(), v[:, c:].contiguous()
         del q, k, qr, kr

@@ -11,13 +11,11 @@ registry instead of two torch slice copies. ``append_fused`` is the
 ``rope/qk_norm_rope_append`` form: the caller's prologue writes k and v into
 the slot in the same pass that produces q and k.
 
-Layout in HBM. Each layer's cache is *stored* head-major, ``[2, B, H, S, D]``,
-and handed out as the ``[2, B, S, H, D]`` view the op API and the model index
-(``head_major_cache``). A decode-shaped attention call streams each head's
-history as one contiguous run instead of 256-byte rows strided ``H*D``
-apart, which on MI355X moves the same bytes about 1.5x faster (measured on a
-load-only kernel at the Wan-5B chunk shape: ~5.0 vs ~3.2 TB/s). Nothing
-outside this class sees the difference: shapes and indexing are unchanged.
+Layout in HBM: the reference's ``[2, B, S, H, D]``, contiguous. A
+head-major store (``[2, B, H, S, D]`` behind the same view, so each head's
+history is one contiguous run) was measured on MI355X at the Wan-5B chunk
+shape and gave no gain (15.77 vs 15.81 us per attention call), so the
+reference layout stays.
 
 Sizing on MI355X: a Wan-5B layer at 1,328 rows is 2 x 1328 x 24 x 128 x 2 B
 = 16.3 MB, so all 30 layers of a long episode fit many times over in 288 GB.
@@ -30,18 +28,11 @@ import torch
 from .. import ops
 
 
-def head_major_cache(batch: int, capacity: int, heads: int, head_dim: int,
-                     device: torch.device | str, dtype: torch.dtype) -> torch.Tensor:
-    """A zeroed ``[2, B, S, H, D]`` cache whose storage is ``[2, B, H, S, D]``."""
-    store = torch.zeros(2, batch, heads, capacity, head_dim, device=device, dtype=dtype)
-    return store.permute(0, 1, 3, 2, 4)
-
-
 class KVCache:
     def __init__(self, layers: int, batch: int, capacity: int, heads: int, head_dim: int,
                  device: torch.device | str, dtype: torch.dtype) -> None:
         self.cache = [
-            head_major_cache(batch, capacity, heads, head_dim, device, dtype)
+            torch.zeros(2, batch, capacity, heads, head_dim, device=device, dtype=dtype)
             for _ in range(layers)
         ]
         self.capacity = capacity

@@ -126,7 +126,8 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  *   mask shape requires. A query with no visible key yields NaN, as the
  *   reference's softmax over an all -inf row does.
  * block_starts: device pointer to n_blocks int32 (starts_dtype DX_I32) or
- * int64 (DX_I64) block start indices, read on the device (no host sync).
+ * int64 (DX_I64) block start indices, read on the device (no host sync),
+ * sorted ascending (the reference builds them with torch.arange).
  * softmax_scale multiplies q.k before the softmax (the reference's default
  * is 1/sqrt(D); callers pass it explicitly). dtype: DX_BF16 or DX_F16;
  * D: 64 or 128.

@@ -140,19 +140,66 @@ def test_split_kv_decode_shape(device, built_lib):
 
 
 def test_head_major_cache_matches_contiguous_bit_exact(device, built_lib):
-    """KVCache stores [2, B, H, S, D] and hands out the [2, B, S, H, D] view;
-    the kernel reads either layout through its strides, with identical results."""
-    from dexter_amd.models.kv_cache import head_major_cache
+    """A cache stored [2, B, H, S, D] and viewed as [2, B, S, H, D] is read
+    through its strides, with results identical to the contiguous layout."""
     b, l, h, d, cache_len = 2, 83, 24, 128, 1245
     q, k, v = (_rand((b, l, h, d), device, seed=s) for s in (43, 44, 45))
     dense = _rand((2, b, cache_len + l, h, d), device, seed=46)
-    hm = head_major_cache(b, cache_len + l, h, d, device, DT)
+    hm = torch.zeros(2, b, h, cache_len + l, d, device=device, dtype=DT).permute(0, 1, 3, 2, 4)
     hm.copy_(dense)
     assert not hm.is_contiguous() and hm.stride(2) == d
     a = ops.blockwise_causal_attention(q, k, v, kv_cache=dense, cache_len=cache_len)
     c = ops.blockwise_causal_attention(q, k, v, kv_cache=hm, cache_len=cache_len)
     assert torch.equal(a, c)
     assert_parity(c, _oracle(q, k, v, dense, cache_len, None))
+
+
+def _decode_case(device, seed=50):
+    b, l, h, d, cache_len = 1, 83, 24, 128, 1245
+    q, k, v = (_rand((b, l, h, d), device, seed=seed + i) for i in range(3))
+    cache = _rand((2, b, cache_len + l, h, d), device, seed=seed + 3)
+    return q, k, v, cache, cache_len
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7, 16])
+def test_split_kv_any_split_count(device, built_lib, monkeypatch, splits):
+    """The merge of split-KV partials for 2..16 splits (16 is the maximum)
+    against the oracle, and bit-identical on a second call."""
+    monkeypatch.setenv("DX_ATTN_SPLITS", str(splits))
+    q, k, v, cache, c = _decode_case(device)
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+    again = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+    assert torch.equal(got, again)
+    assert_parity(got, _oracle(q, k, v, cache, c, None), what=f"{splits} splits")
+
+
+def test_split_kv_graph_replays_match_eager(device, built_lib):
+    """A captured decode call replayed several times, with other split-KV work
+    (a ragged batch) run eagerly between replays: every replay equals the
+    eager result bit for bit."""
+    q, k, v, cache, c = _decode_case(device)
+    eager = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+    lens = [83, 1245, 415]
+    qv, kv_, vv = (_rand((3, 99, 8, 128), device, seed=60 + i) for i in range(3))
+    cv = _rand((2, 3, 1245, 8, 128), device, seed=63)
+    other_ref = ops.blockwise_causal_attention_varlen(qv, kv_, vv, kv_cache=cv, cache_lens=lens)
+    out = {}
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):  # warm the capture stream's workspace outside capture
+        ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        out["o"] = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out["o"], eager), f"replay {i}"
+        other = ops.blockwise_causal_attention_varlen(qv, kv_, vv, kv_cache=cv, cache_lens=lens)
+        torch.cuda.synchronize()
+        assert torch.equal(other, other_ref)
 
 
 def test_rows_before_the_first_block_match_the_reference(device, built_lib):
