@@ -54,10 +54,12 @@
 // sequence with its own split count, longest sequence first.
 #include "dx_common.h"
 
+#include <float.h>
 #include <stdlib.h>
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace dx {
@@ -105,6 +107,12 @@ template <> struct Mfma<bf16_t> {
     bf16x2 r = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
     return __builtin_bit_cast(uint32_t, r);
   }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_bf16 against (1, 1)).
+  static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+  }
 };
 template <> struct Mfma<f16_t> {
   static __device__ __forceinline__ f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
@@ -115,6 +123,12 @@ template <> struct Mfma<f16_t> {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     f16x2 r = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
     return __builtin_bit_cast(uint32_t, r);
+  }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_f16 against (1, 1)).
+  static __device__ __forceinline__ float sum2(uint32_t p, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p),
+                                  __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
   }
 };
 
@@ -210,9 +224,13 @@ struct TileRegs {
   __device__ __forceinline__ void load(int tid, const KvSrc& src, int t, bool live) {
     const int r0 = tid / CPR, colb = (tid % CPR) * 16;
     const bool in_cache = t < src.n_ct;
-    __amdgpu_buffer_rsrc_t rk = in_cache ? src.kc : src.kn;
-    __amdgpu_buffer_rsrc_t rv = in_cache ? src.vc : src.vn;
-    if (!live) rk = rv = src.none;
+    // Value selects (not a select of member addresses, which would keep the
+    // descriptors in scratch memory).
+    const __amdgpu_buffer_rsrc_t kc = src.kc, kn = src.kn, vc = src.vc, vn = src.vn;
+    const __amdgpu_buffer_rsrc_t none = src.none;
+    __amdgpu_buffer_rsrc_t rk = in_cache ? kc : kn;
+    __amdgpu_buffer_rsrc_t rv = in_cache ? vc : vn;
+    if (!live) rk = rv = none;
     const int sk = in_cache ? src.c_ss2 : src.k_sl2;
     const int sv = in_cache ? src.c_ss2 : src.v_sl2;
     const int row = (in_cache ? t : t - src.n_ct) * kBN + r0;
@@ -224,6 +242,44 @@ struct TileRegs {
     }
   }
 
+  // K or V alone (the pipelined single-stream loop keeps them a tile apart).
+  __device__ __forceinline__ void loadK(int tid, const KvSrc& src, int t, bool live) {
+    const int r0 = tid / CPR, colb = (tid % CPR) * 16;
+    const bool in_cache = t < src.n_ct;
+    const __amdgpu_buffer_rsrc_t kc = src.kc, kn = src.kn, none = src.none;
+    __amdgpu_buffer_rsrc_t rk = in_cache ? kc : kn;
+    if (!live) rk = none;
+    const int sk = in_cache ? src.c_ss2 : src.k_sl2;
+    const int ok = ((in_cache ? t : t - src.n_ct) * kBN + r0) * sk + colb;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) kr[i] = buf_load16(rk, ok + i * RPI * sk);
+  }
+  __device__ __forceinline__ void loadV(int tid, const KvSrc& src, int t, bool live) {
+    const int r0 = tid / CPR, colb = (tid % CPR) * 16;
+    const bool in_cache = t < src.n_ct;
+    const __amdgpu_buffer_rsrc_t vc = src.vc, vn = src.vn, none = src.none;
+    __amdgpu_buffer_rsrc_t rv = in_cache ? vc : vn;
+    if (!live) rv = none;
+    const int sv = in_cache ? src.c_ss2 : src.v_sl2;
+    const int ov = ((in_cache ? t : t - src.n_ct) * kBN + r0) * sv + colb;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) vr[i] = buf_load16(rv, ov + i * RPI * sv);
+  }
+  __device__ __forceinline__ void storeK(int tid, uint16_t* Ks) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NT;
+      *reinterpret_cast<u32x4*>(Ks + (c / CPR) * Lds<D>::kPitch + (c % CPR) * 8) = kr[i];
+    }
+  }
+  __device__ __forceinline__ void storeV(int tid, uint16_t* Vs) const {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NT;
+      *reinterpret_cast<u32x4*>(Vs + (c / CPR) * Lds<D>::vPitch + (c % CPR) * 8) = vr[i];
+    }
+  }
+
   __device__ __forceinline__ void store(int tid, uint16_t* Ks, uint16_t* Vs) const {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -232,6 +288,79 @@ struct TileRegs {
       *reinterpret_cast<u32x4*>(Ks + row * Lds<D>::kPitch + col) = kr[i];
       *reinterpret_cast<u32x4*>(Vs + row * Lds<D>::vPitch + col) = vr[i];
     }
+  }
+};
+
+// Direct global -> LDS tile loads (gfx950 buffer_load_dwordx4 ... lds, no
+// registers in between). One such instruction moves 64 lanes x 16 bytes into
+// 1 KB of LDS at M0 + 16 lane, while each lane's global offset is free: the
+// padded tile layout (K rows of kPitch, V rows of vPitch elements) is cut
+// into 1 KB pieces, and lane l of piece q fetches whatever row/column lands
+// at byte 1024 q + 16 l -- or, for a padding slot, an offset past every
+// buffer's end, which writes zeros. Rows past a descriptor's bound read as
+// zeros too. The four waves of a stream take pieces w, w + 4, ...; each
+// thread keeps its (row, byte column) per piece, packed, -1 for padding.
+// Completion is tracked by vmcnt: a wave waits for its own pieces before the
+// barrier that publishes the tile.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Templated on the element type too, although nothing in it depends on T:
+// with one TileDma<D> shared by the bf16 and f16 kernels, hipcc (ROCm 7.2)
+// silently drops the host-side stub of whichever kernel instantiates it
+// second, leaving an undefined symbol in the library.
+template <int D, typename T>
+struct TileDma {
+  static constexpr int KSL = Lds<D>::kPitch / 8;  // 16-byte slots per K row
+  static constexpr int VSL = Lds<D>::vPitch / 8;
+  static constexpr int KQ = kBN * KSL / 64;       // pieces per K tile
+  static constexpr int VQ = kBN * VSL / 64;
+  static constexpr int KM = (KQ + kNW - 1) / kNW;  // pieces per wave (at most)
+  static constexpr int VM = (VQ + kNW - 1) / kNW;
+  static_assert(kBN * KSL % 64 == 0 && kBN * VSL % 64 == 0, "tiles must be whole pieces");
+  static constexpr uint32_t kPast = 0x80000000u;  // beyond any descriptor's records
+  int kp[KM], vp[VM];  // (row << 16) | byte column, or -1
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+#pragma unroll
+    for (int m = 0; m < KM; ++m) {
+      const int x = (wave + kNW * m) * 64 + lane, row = x / KSL, sl = x % KSL;
+      kp[m] = sl < D / 8 ? (row << 16) | (sl * 16) : -1;
+    }
+#pragma unroll
+    for (int m = 0; m < VM; ++m) {
+      const int x = (wave + kNW * m) * 64 + lane, row = x / VSL, sl = x % VSL;
+      vp[m] = sl < D / 8 ? (row << 16) | (sl * 16) : -1;
+    }
+  }
+  __device__ __forceinline__ static uint32_t offset(int pc, int row0, int stride) {
+    return pc < 0 ? kPast : uint32_t((row0 + (pc >> 16)) * stride + (pc & 0xffff));
+  }
+  // Tile t's K into Ks (and V into Vs) from wave ``wave`` of the stream.
+  __device__ __forceinline__ void issueK(const KvSrc& src, int t, int wave, uint16_t* Ks) const {
+    const bool in_cache = t < src.n_ct;
+    const __amdgpu_buffer_rsrc_t kc = src.kc, kn = src.kn;
+    const __amdgpu_buffer_rsrc_t rk = in_cache ? kc : kn;
+    const int stride = in_cache ? src.c_ss2 : src.k_sl2;
+    const int row0 = (in_cache ? t : t - src.n_ct) * kBN;
+#pragma unroll
+    for (int m = 0; m < KM; ++m)
+      if (kNW * m + kNW - 1 < KQ || wave + kNW * m < KQ)  // first: always true, known at compile time
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (lds_void_t*)(Ks + (wave + kNW * m) * 512), 16, offset(kp[m], row0, stride), 0,
+            0, 0);
+  }
+  __device__ __forceinline__ void issueV(const KvSrc& src, int t, int wave, uint16_t* Vs) const {
+    const bool in_cache = t < src.n_ct;
+    const __amdgpu_buffer_rsrc_t vc = src.vc, vn = src.vn;
+    const __amdgpu_buffer_rsrc_t rv = in_cache ? vc : vn;
+    const int stride = in_cache ? src.c_ss2 : src.v_sl2;
+    const int row0 = (in_cache ? t : t - src.n_ct) * kBN;
+#pragma unroll
+    for (int m = 0; m < VM; ++m)
+      if (kNW * m + kNW - 1 < VQ || wave + kNW * m < VQ)  // first: always true, known at compile time
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rv, (lds_void_t*)(Vs + (wave + kNW * m) * 512), 16, offset(vp[m], row0, stride), 0,
+            0, 0);
   }
 };
 
@@ -310,36 +439,60 @@ struct Softmax {
   float l;  // sum of exponentials (this lane's half of the keys)
 };
 
-// One key tile: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// The phases of one key tile, for one wave (32 queries):
+//   qk_tile      S^T = K Q^T (16 MFMAs for D = 128), K read from LDS;
+//   softmax_max  per-key masking, row max, lazy rescale of acc;
+//   softmax_exp  P = exp2(S c - ref) in place, row sum;
+//   pv_tile      O^T += V^T P^T (16 MFMAs), V^T gathered by transposing reads.
 // ``masked``: some key of the tile is invisible to some query of the
 // workgroup (a straddling tile; workgroup-uniform). Unmasked tiles do no
 // per-key visibility work.
+
 template <int D, typename T>
-__device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs,
-                                          const u32x4 (&qr)[D / 16], f32x16 (&acc)[D / 32],
-                                          Softmax& sm, float c, int lim_rel, bool masked,
-                                          int lane) {
-  constexpr int KS = D / 16, DT = D / 32;
+__device__ __forceinline__ void qk_tile(const uint16_t* Ks, const u32x4 (&qr)[D / 16],
+                                        f32x16 (&s)[2], int lane) {
+  constexpr int KS = D / 16;
+  constexpr int N = 2 * KS;  // MFMAs: (half kt, k-step ks) = (i / KS, i % KS)
+  constexpr int W = 4;       // K fragments in flight ahead of the MFMA using them
   const int n = lane & 31, g = lane >> 5;
-  f32x16 s[2];
+  const uint16_t* kp = Ks + n * Lds<D>::kPitch + 8 * g;
+  auto frag = [&](int i) __attribute__((always_inline)) {
+    return *reinterpret_cast<const u32x4*>(kp + (i / KS) * 32 * Lds<D>::kPitch + 16 * (i % KS));
+  };
+  u32x4 kf[W];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    s[kt] = f32x16{};
-    const uint16_t* kp = Ks + (32 * kt + n) * Lds<D>::kPitch + 8 * g;
+  for (int i = 0; i < W; ++i) kf[i] = frag(i);
+  s[0] = f32x16{};
+  s[1] = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      s[kt] = Mfma<T>::run(*reinterpret_cast<const u32x4*>(kp + 16 * ks), qr[ks], s[kt]);
+  for (int i = 0; i < N; ++i) {
+    s[i / KS] = Mfma<T>::run(kf[i % W], qr[i % KS], s[i / KS]);
+    if (i + W < N) kf[i % W] = frag(i + W);
   }
-  // Key of register r of half kt: row 32 kt + 8 (r / 4) + 4 g + r % 4 of the
-  // tile, visible iff that row is below lim_rel (rows past the tile's valid
-  // keys or past this query's visible end are not).
-  const int lim = lim_rel - 4 * g;
+}
+
+// Key of register r of half kt: row 32 kt + 8 (r / 4) + 4 g + r % 4 of the
+// tile, visible iff that row is below lim_rel (rows past the tile's valid
+// keys or past this query's visible end are not). ``lim`` is lim_rel - 4 g.
+__device__ __forceinline__ bool key_hidden(int kt, int r, int lim) {
+  return 32 * kt + 8 * (r / 4) + (r % 4) >= lim;
+}
+
+// Returns the exponent base (max in log2 units, 0 while nothing is visible).
+template <int D>
+__device__ __forceinline__ float softmax_max(f32x16 (&s)[2], f32x16 (&acc)[D / 32],
+                                             Softmax& sm, float c, int lim, bool masked) {
+  constexpr int DT = D / 32;
   if (masked) {
+    // The compare operand is fenced into this branch so that the compiler
+    // does not compute the 32 compares for unmasked tiles too.
+    int l = lim;
+    asm volatile("" : "+v"(l));
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (32 * kt + 8 * (r / 4) + (r % 4) >= lim) s[kt][r] = -INFINITY;
+        if (key_hidden(kt, r, l)) s[kt][r] = -INFINITY;
   }
   // Row max over the visible scores (raw units; c >= 0 keeps the order).
   float tmax = -INFINITY;
@@ -363,30 +516,34 @@ __device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs
     sm.m = m_new;
   }
   // Nothing visible yet: exponent base 0.
-  const float mb = sm.m == -INFINITY ? 0.f : sm.m * c;
+  return sm.m == -INFINITY ? 0.f : sm.m * c;
+}
+
+// Masked scores are -inf and c > 0 (the host guarantees it), so their
+// exponentials are exactly 0 with no further masking.
+__device__ __forceinline__ void softmax_exp(f32x16 (&s)[2], Softmax& sm, float c, float mb) {
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kt][r] = fast_exp2(__builtin_fmaf(s[kt][r], c, -mb));
-  // exp2(-inf * c) is 0 for c > 0 but NaN for c == 0: zero masked p explicitly.
-  if (masked) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (32 * kt + 8 * (r / 4) + (r % 4) >= lim) s[kt][r] = 0.f;
-  }
   float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) part[r % 4] += s[kt][r];
   sm.l += (part[0] + part[1]) + (part[2] + part[3]);
-  // O^T += V^T P^T, 16 keys per MFMA (key step u = 2 kt + hf). The A
-  // operand of lane (n, g) is head_dim column 32 d + n at keys
-  // 16u + {4g..4g+3, 8+4g..8+4g+3}, gathered from the row-major V tile by two
-  // transposing reads: lane j of each 16-lane group addresses key
-  // 16u + 8r + 4g + j/4 (r = 0, 1) at dims 32 d + 16 ((lane/16) % 2) + 4 (j % 4).
+}
+
+// O^T += V^T P^T, 16 keys per MFMA (key step u = 2 kt + hf). The A operand
+// of lane (n, g) is head_dim column 32 d + n at keys
+// 16u + {4g..4g+3, 8+4g..8+4g+3}, gathered from the row-major V tile by two
+// transposing reads: lane j of each 16-lane group addresses key
+// 16u + 8r + 4g + j/4 (r = 0, 1) at dims 32 d + 16 ((lane/16) % 2) + 4 (j % 4).
+template <int D, typename T>
+__device__ __forceinline__ void pv_tile(const uint16_t* Vs, const f32x16 (&s)[2],
+                                        f32x16 (&acc)[D / 32], int lane) {
+  constexpr int DT = D / 32;
+  const int g = lane >> 5;
   const int j = lane & 15, half = (lane >> 4) & 1;
   const uint16_t* vbase = Vs + (4 * g + (j >> 2)) * Lds<D>::vPitch + 16 * half + 4 * (j & 3);
 #pragma unroll
@@ -405,6 +562,116 @@ __device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs
         acc[d] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, acc[d]);
       }
     }
+}
+
+// The straight-line middle of a pipelined step, one basic block:
+//   S_next = K_next Q^T            (HasNext; 2*KS MFMAs, K from LDS)
+//   P = exp2(S c - mb), packed     (32 v_exp per lane, v_cvt_pk)
+//   l += row sum of the packed P   (v_dot2 against (1, 1): 2 keys per op)
+//   O^T += V^T P^T                 (16 MFMAs, V^T by transposing reads)
+// Masked scores are already -inf and c > 0, so their P is exactly 0. The
+// sched_group_barrier sequence at the end interleaves the QK^T MFMAs with the
+// exponentials and the PV MFMAs with the packing, so one wave keeps its SIMD's
+// matrix pipe busy while its vector pipe works, and runs LDS reads ahead.
+namespace sg {
+constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100;
+}
+
+template <int D, typename T, bool HasNext>
+__device__ __forceinline__ void step_body(const uint16_t* Kn, const uint16_t* Vs,
+                                          const u32x4 (&qr)[D / 16], f32x16 (&cur)[2],
+                                          f32x16 (&nxt)[2], f32x16 (&acc)[D / 32],
+                                          Softmax& sm, float c, float mb, int lane) {
+  constexpr int KS = D / 16, DT = D / 32;
+  constexpr int NQ = 2 * KS;  // QK^T MFMAs
+  constexpr int W = 4;        // K fragments in flight
+  const int n = lane & 31, g = lane >> 5;
+  // S_next: MFMA i is (half i / KS, k-step i % KS).
+  const uint16_t* kp = Kn + n * Lds<D>::kPitch + 8 * g;
+  auto frag = [&](int i) __attribute__((always_inline)) {
+    return *reinterpret_cast<const u32x4*>(kp + (i / KS) * 32 * Lds<D>::kPitch + 16 * (i % KS));
+  };
+  if (HasNext) {
+    u32x4 kf[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) kf[i] = frag(i);
+    nxt[0] = f32x16{};
+    nxt[1] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      nxt[i / KS] = Mfma<T>::run(kf[i % W], qr[i % KS], nxt[i / KS]);
+      if (i + W < NQ) kf[i % W] = frag(i + W);
+    }
+  }
+  // P and its row sum.
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cur[kt][r] = fast_exp2(__builtin_fmaf(cur[kt][r], c, -mb));
+  // Region 1 schedule: each QK^T MFMA followed by 4 of the 64 fma/exp ops,
+  // with the K reads W MFMAs ahead. The full scheduling barrier after it
+  // keeps region 2's V^T reads from being hoisted here (which would hold
+  // them in registers through region 1).
+  if (HasNext) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 1, 0);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      __builtin_amdgcn_sched_group_barrier(sg::kMfma, 1, 0);
+      if (i + W < NQ) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(sg::kValu, 4, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 pk[4];  // pk[2 kt + hf][e]: keys 8 hf + 2 e, +1 of half kt
+  float part[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t p =
+          Mfma<T>::pack(cur[u / 2][8 * (u % 2) + 2 * e], cur[u / 2][8 * (u % 2) + 2 * e + 1]);
+      pk[u][e] = p;
+      part[e & 1] = Mfma<T>::sum2(p, part[e & 1]);
+    }
+  sm.l += part[0] + part[1];
+  // O^T += V^T P^T (see pv_tile for the operand layout).
+  const int j = lane & 15, half = (lane >> 4) & 1;
+  const uint16_t* vbase = Vs + (4 * g + (j >> 2)) * Lds<D>::vPitch + 16 * half + 4 * (j & 3);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint16_t* vu = vbase + 16 * u * Lds<D>::vPitch;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const u32x2 lo = lds_read_tr16(vu + 32 * d);
+      const u32x2 hi = lds_read_tr16(vu + 8 * Lds<D>::vPitch + 32 * d);
+      acc[d] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[u], acc[d]);
+    }
+  }
+  // Region 2 schedule: the V^T reads two MFMAs ahead of the PV MFMAs, with
+  // the packing and sums spread between them.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 1, 0);
+  __builtin_amdgcn_sched_group_barrier(sg::kValu, 8, 0);
+#pragma unroll
+  for (int i = 0; i < 4 * DT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(sg::kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(sg::kValu, 2, 0);
+  }
+}
+
+// One whole key tile (the dual-stream decode path).
+template <int D, typename T>
+__device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs,
+                                          const u32x4 (&qr)[D / 16], f32x16 (&acc)[D / 32],
+                                          Softmax& sm, float c, int lim, bool masked,
+                                          int lane) {
+  f32x16 s[2];
+  qk_tile<D, T>(Ks, qr, s, lane);
+  const float mb = softmax_max<D>(s, acc, sm, c, lim, masked);
+  softmax_exp(s, sm, c, mb);
+  pv_tile<D, T>(Vs, s, acc, lane);
 }
 
 template <int D, typename T, int NS>
@@ -483,7 +750,17 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 
   TileRegs<D> regs;
   const int t_first = t_begin + stream;
-  regs.load(ltid, src, t_first, t_first < t_end);
+  TileDma<D, T> dma;
+  if constexpr (NS == 1) {
+    // The first tile straight into LDS.
+    dma.init(wave, lane);
+    if (t_begin < t_end) {
+      dma.issueK(src, t_begin, wave, smem);
+      dma.issueV(src, t_begin, wave, smem + Lds<D>::kElems);
+    }
+  } else {
+    regs.load(ltid, src, t_first, t_first < t_end);
+  }
 
   // Visible-key end of this lane's query (per-key masking of straddling tiles).
   const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
@@ -522,6 +799,45 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   Softmax sm{-INFINITY, 0.f};
   const float c = a.scale_log2;
 
+  // Key tile t's masking: cache tiles see every cached key and only the
+  // partial last one masks (its rows past cache_len); new-key tiles mask
+  // where they reach past kv_min.
+  auto tile_mask = [&](int t, int& lim, bool& masked) __attribute__((always_inline)) {
+    const bool in_cache = t < n_ct;
+    const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
+    lim = (in_cache ? cache_len - j0 : my_end - j0) - 4 * g;
+    masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
+  };
+
+  if constexpr (NS == 1) {
+    // Double buffer filled by LDS DMA: step i first sends tile i + 1 into
+    // the buffer that tile i - 1 used (every wave finished reading it before
+    // the barrier that ended step i - 1), computes tile i, then waits for its
+    // own pieces and meets the other waves at the barrier that publishes
+    // tile i + 1.
+    const int nt = t_end - t_begin;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of the first tile
+    __syncthreads();
+    for (int i = 0; i < nt; ++i) {
+      uint16_t* const cur = smem + (i & 1) * Lds<D>::stage;
+      uint16_t* const nxt = smem + ((i + 1) & 1) * Lds<D>::stage;
+      if (i + 1 < nt) {
+        dma.issueK(src, t_begin + i + 1, wave, nxt);
+        dma.issueV(src, t_begin + i + 1, wave, nxt + Lds<D>::kElems);
+      }
+      if (wave_active) {
+        int lim;
+        bool masked;
+        tile_mask(t_begin + i, lim, masked);
+        f32x16 sc[2];
+        qk_tile<D, T>(cur, qr, sc, lane);
+        const float mb = softmax_max<D>(sc, acc, sm, c, lim, masked);
+        step_body<D, T, false>(cur, cur + Lds<D>::kElems, qr, sc, sc, acc, sm, c, mb, lane);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  } else {
   // Each stream double-buffers its tiles in its own LDS region. A buffer is
   // rewritten two rounds after it was read, past the barrier of the round in
   // between, which every wave has reached.
@@ -533,15 +849,12 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     __syncthreads();
     if (t + NS < t_end) regs.load(ltid, src, t + NS, true);
     if (wave_active && t < t_end) {
-      // Cache tiles: every query sees every cached key; only the partial
-      // last one masks (its rows past cache_len). New-key tiles mask where
-      // they reach past kv_min.
-      const bool in_cache = t < n_ct;
-      const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
-      const int lim_rel = in_cache ? cache_len - j0 : my_end - j0;
-      const bool masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
-      tile_step<D, T>(st, st + Lds<D>::kElems, qr, acc, sm, c, lim_rel, masked, lane);
+      int lim;
+      bool masked;
+      tile_mask(t, lim, masked);
+      tile_step<D, T>(st, st + Lds<D>::kElems, qr, acc, sm, c, lim, masked, lane);
     }
+  }
   }
 
   // The exponent reference of acc and l, in log2 units.
@@ -920,7 +1233,12 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   // A negative scale enters as a negated q (exact) and |scale|, so the kernel
   // only ever multiplies scores by a non-negative factor.
   a.negate_q = softmax_scale < 0.f;
-  a.scale_log2 = fabsf(softmax_scale) * 1.4426950408889634f;
+  // The kernel multiplies scores by c = |scale| log2(e) and relies on c > 0
+  // (masked scores are -inf, and exp2(-inf * c) must be 0, not NaN). A zero
+  // scale becomes the smallest normal float: every finite score times it is
+  // below 2^-24 in magnitude, so each visible key still gets exp2(~0) = 1
+  // exactly -- the reference's uniform softmax over the visible keys.
+  a.scale_log2 = std::max(fabsf(softmax_scale) * 1.4426950408889634f, FLT_MIN);
   a.cache_len = int(cache_len);
   a.n_splits = p.uniform_splits;
   a.n_seg = p.n_seg;

@@ -37,6 +37,19 @@ def test_library_exports_every_declared_symbol(built_lib):
     assert not missing, f"not exported: {missing}"
 
 
+def test_library_resolves_all_of_its_own_symbols(built_lib):
+    """No kernel or stub of the library's own namespace is left undefined (a
+    dropped template instantiation links, then fails at load on the GPU box)."""
+    import shutil
+    import subprocess
+    if shutil.which("nm") is None:
+        pytest.skip("nm not available")
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(built_lib)], capture_output=True,
+                         text=True, check=True).stdout
+    own = [line.split()[-1] for line in out.splitlines() if "_ZN2dx" in line]
+    assert not own, f"undefined: {own}"
+
+
 def test_loader_binds_exactly_the_header(built_lib):
     assert sorted(_lib.exported_symbols()) == declared_functions()
 
