@@ -77,12 +77,13 @@ struct AttnArgs {
   const uint16_t* v; int64_t v_sb, v_sl, v_sh;
   const uint16_t* ck; const uint16_t* cv; int64_t c_sb, c_ss, c_sh;
   uint16_t* out; int64_t o_sb, o_sl, o_sh;
-  uint16_t* ws_o;  // [partials][kBM][D] f16 normalised partial outputs acc / l
-  float* ws_ml;    // [partials][kBM][2] (exponent reference in log2 units, sum l)
+  uint16_t* ws_o;  // [partials][bm][D] f16 normalised partial outputs acc / l
+  float* ws_ml;    // [partials][bm][2] (exponent reference in log2 units, sum l)
   const void* starts; int starts_i64; int n_blocks;
   int B, H, Lq, Lk;
   int causal;
   int n_qtiles;
+  int bm;            // queries per work item: 128 (dual-stream decode) or 256 (paired groups)
   float scale_log2;  // |softmax scale| * log2(e)
   int negate_q;      // softmax scale < 0: q enters negated (exact), scale as |scale|
   int cache_len;     // uniform mode
@@ -304,18 +305,37 @@ struct TileRegs {
 // barrier that publishes the tile.
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// One DMA piece: 64 lanes x 16 bytes from the buffer at per-lane offsets into
+// LDS bytes [lds, lds + 1024). Written as inline assembly on purpose: the
+// compiler's wait-count pass treats the builtin form as an LDS write of
+// unknown extent and puts a full vmcnt wait before every later LDS read,
+// which would stall each tile's reads on the next tile's still-flying
+// pieces. The callers wait for their pieces explicitly (s_waitcnt before the
+// barrier that publishes them). M0 holds the LDS base; nothing else in these
+// kernels uses M0 (gfx9 LDS instructions do not read it), and the s_nop is
+// the one wait state an LDS DMA needs after M0 is written.
+__device__ __forceinline__ void dma_piece(__amdgpu_buffer_rsrc_t rsrc, const uint16_t* lds,
+                                          uint32_t voff) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(
+      uint32_t(uintptr_t((__attribute__((address_space(3))) const uint16_t*)lds)));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(base), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
 // Templated on the element type too, although nothing in it depends on T:
 // with one TileDma<D> shared by the bf16 and f16 kernels, hipcc (ROCm 7.2)
 // silently drops the host-side stub of whichever kernel instantiates it
 // second, leaving an undefined symbol in the library.
-template <int D, typename T>
+template <int D, typename T, int NWV = kNW>  // NWV waves share each tile's pieces
 struct TileDma {
   static constexpr int KSL = Lds<D>::kPitch / 8;  // 16-byte slots per K row
   static constexpr int VSL = Lds<D>::vPitch / 8;
   static constexpr int KQ = kBN * KSL / 64;       // pieces per K tile
   static constexpr int VQ = kBN * VSL / 64;
-  static constexpr int KM = (KQ + kNW - 1) / kNW;  // pieces per wave (at most)
-  static constexpr int VM = (VQ + kNW - 1) / kNW;
+  static constexpr int KM = (KQ + NWV - 1) / NWV;  // pieces per wave (at most)
+  static constexpr int VM = (VQ + NWV - 1) / NWV;
   static_assert(kBN * KSL % 64 == 0 && kBN * VSL % 64 == 0, "tiles must be whole pieces");
   static constexpr uint32_t kPast = 0x80000000u;  // beyond any descriptor's records
   int kp[KM], vp[VM];  // (row << 16) | byte column, or -1
@@ -323,12 +343,12 @@ struct TileDma {
   __device__ __forceinline__ void init(int wave, int lane) {
 #pragma unroll
     for (int m = 0; m < KM; ++m) {
-      const int x = (wave + kNW * m) * 64 + lane, row = x / KSL, sl = x % KSL;
+      const int x = (wave + NWV * m) * 64 + lane, row = x / KSL, sl = x % KSL;
       kp[m] = sl < D / 8 ? (row << 16) | (sl * 16) : -1;
     }
 #pragma unroll
     for (int m = 0; m < VM; ++m) {
-      const int x = (wave + kNW * m) * 64 + lane, row = x / VSL, sl = x % VSL;
+      const int x = (wave + NWV * m) * 64 + lane, row = x / VSL, sl = x % VSL;
       vp[m] = sl < D / 8 ? (row << 16) | (sl * 16) : -1;
     }
   }
@@ -344,10 +364,8 @@ struct TileDma {
     const int row0 = (in_cache ? t : t - src.n_ct) * kBN;
 #pragma unroll
     for (int m = 0; m < KM; ++m)
-      if (kNW * m + kNW - 1 < KQ || wave + kNW * m < KQ)  // first: always true, known at compile time
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rk, (lds_void_t*)(Ks + (wave + kNW * m) * 512), 16, offset(kp[m], row0, stride), 0,
-            0, 0);
+      if (NWV * m + NWV - 1 < KQ || wave + NWV * m < KQ)  // first: always true, known at compile time
+        dma_piece(rk, Ks + (wave + NWV * m) * 512, offset(kp[m], row0, stride));
   }
   __device__ __forceinline__ void issueV(const KvSrc& src, int t, int wave, uint16_t* Vs) const {
     const bool in_cache = t < src.n_ct;
@@ -357,10 +375,8 @@ struct TileDma {
     const int row0 = (in_cache ? t : t - src.n_ct) * kBN;
 #pragma unroll
     for (int m = 0; m < VM; ++m)
-      if (kNW * m + kNW - 1 < VQ || wave + kNW * m < VQ)  // first: always true, known at compile time
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rv, (lds_void_t*)(Vs + (wave + kNW * m) * 512), 16, offset(vp[m], row0, stride), 0,
-            0, 0);
+      if (NWV * m + NWV - 1 < VQ || wave + NWV * m < VQ)  // first: always true, known at compile time
+        dma_piece(rv, Vs + (wave + NWV * m) * 512, offset(vp[m], row0, stride));
   }
 };
 
@@ -674,6 +690,50 @@ __device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs
   pv_tile<D, T>(Vs, s, acc, lane);
 }
 
+// A lane's result for its query qi (row ``row`` of the work item's BM
+// queries): the output, or with split-KV the normalised partial in f16
+// (|value| <= max |v|, 11-bit mantissa) plus (reference, l) in fp32, which the
+// merge re-weights by l. No visible key: partial o = 0, reference -inf; final
+// output NaN (0 * inf), as the reference.
+template <int D, typename T>
+__device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it, int bm, int row,
+                                             int qi, int g, const f32x16 (&acc)[D / 32],
+                                             float l_tot, float mref) {
+  constexpr int DT = D / 32;
+  if (it.n_splits == 1) {
+    const float inv = 1.0f / l_tot;
+    uint16_t* op = a.out + it.b * a.o_sb + int64_t(qi) * a.o_sl + it.h * a.o_sh;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int dim = 32 * d + 8 * r4 + 4 * g;
+        u32x2 w;
+        w[0] = Mfma<T>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
+        w[1] = Mfma<T>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + dim) = w;
+      }
+  } else {
+    const int64_t pidx = it.pbase + it.split;
+    const bool any = l_tot > 0.f;
+    const float inv = any ? 1.0f / l_tot : 0.f;
+    uint16_t* po = a.ws_o + (pidx * bm + row) * D;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int dim = 32 * d + 8 * r4 + 4 * g;
+        u32x2 w;
+        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
+        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(po + dim) = w;
+      }
+    if (g == 0)
+      *reinterpret_cast<float2*>(a.ws_ml + (pidx * bm + row) * 2) =
+          make_float2(any ? mref : -INFINITY, l_tot);
+  }
+}
+
 template <int D, typename T, int NS>
 __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
@@ -890,48 +950,325 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 
   const float l_tot = sm.l + __shfl_xor(sm.l, 32, 64);
   if (!qvalid) return;
-  if (it.n_splits == 1) {
-    const float inv = 1.0f / l_tot;  // 0 visible keys: 0 * inf = NaN, as the reference
-    uint16_t* op = a.out + b * a.o_sb + int64_t(qi) * a.o_sl + h * a.o_sh;
+  store_result<D, T>(a, it, kBM, wave * 32 + n, qi, g, acc, l_tot, mref);
+}
+
+// ---------------------------------------------------------------------------
+// Prefill: two groups of four waves on the same key tiles, half a tile apart.
+//
+// A workgroup covers 256 queries: group 0 takes rows 0..127, group 1 rows
+// 128..255, and both read each K/V tile from LDS (one DMA fill per tile for
+// 256 queries). Each group alternates two phases per key tile:
+//   MFMA phase  PV of the previous tile and S = K Q^T of this one (32 MFMAs)
+//   VALU phase  masking, row max, lazy rescale, exponentials, packing, sums
+// and group 1 runs one phase behind group 0, with a workgroup barrier
+// between phases. Waves w and w + 4 share a SIMD, so on every SIMD one wave's
+// MFMAs overlap the other wave's vector work: the phases are arranged so the
+// matrix pipe and the vector pipe of a SIMD are busy at the same time, which
+// one wave alone cannot do (in-order issue puts its dependent softmax after
+// its MFMAs).
+//
+// Buffers: K and V are double buffered separately. Tile j's K is read in
+// global phases 2j-1 (group 0) and 2j (group 1); its V in 2j+1 and 2j+2. In
+// each odd phase 2m+1 every wave sends its DMA pieces of K_{m+2} (into the K
+// buffer K_m left at the barrier ending phase 2m) and V_{m+1} (into V_{m-1}'s
+// buffer, free since then too), and waits for them at the end of phase 2m+2:
+// two phases of latency cover, nothing overwritten while read.
+// ---------------------------------------------------------------------------
+constexpr int kPairWaves = 8;
+constexpr int kBMPair = 256;
+
+// P = exp2(S c - mb) packed to 16-bit pairs in MFMA B-operand order (pk[u][e]:
+// keys 8 (u % 2) + 2 e, +1 of half u / 2) and the row sum over the packed
+// values (v_dot2 against (1, 1): l sums exactly the P used by PV). Masked
+// scores are -inf and c > 0, so their P is exactly 0.
+template <typename T>
+__device__ __forceinline__ void exp_pack(f32x16 (&s)[2], Softmax& sm, float c, float mb,
+                                         u32x4 (&pk)[4]) {
 #pragma unroll
-    for (int d = 0; d < DT; ++d)
+  for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int dim = 32 * d + 8 * r4 + 4 * g;
-        u32x2 w;
-        w[0] = Mfma<T>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
-        w[1] = Mfma<T>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + dim) = w;
-      }
-  } else {
-    // Split-KV partial: the normalised output acc / l of this key range in
-    // f16 (|value| <= max |v|, 11-bit mantissa) plus (reference, l) in fp32;
-    // the merge re-weights by l. No visible key: o = 0, reference -inf.
-    const int64_t pidx = it.pbase + it.split;
-    const int row = wave * 32 + n;
-    const bool any = l_tot > 0.f;
-    const float inv = any ? 1.0f / l_tot : 0.f;
-    uint16_t* po = a.ws_o + (pidx * kBM + row) * D;
+    for (int r = 0; r < 16; ++r) s[kt][r] = fast_exp2(__builtin_fmaf(s[kt][r], c, -mb));
+  float part[2] = {0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < DT; ++d)
+  for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int dim = 32 * d + 8 * r4 + 4 * g;
-        u32x2 w;
-        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
-        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(po + dim) = w;
-      }
-    if (g == 0)
-      *reinterpret_cast<float2*>(a.ws_ml + (pidx * kBM + row) * 2) =
-          make_float2(any ? mref : -INFINITY, l_tot);
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t p =
+          Mfma<T>::pack(s[u / 2][8 * (u % 2) + 2 * e], s[u / 2][8 * (u % 2) + 2 * e + 1]);
+      pk[u][e] = p;
+      part[e & 1] = Mfma<T>::sum2(p, part[e & 1]);
+    }
+  sm.l += part[0] + part[1];
+}
+
+// O^T += V^T P^T from packed P (operand layout as pv_tile).
+template <int D, typename T>
+__device__ __forceinline__ void pv_packed(const uint16_t* Vs, const u32x4 (&pk)[4],
+                                          f32x16 (&acc)[D / 32], int lane) {
+  constexpr int DT = D / 32;
+  const int g = lane >> 5;
+  const int j = lane & 15, half = (lane >> 4) & 1;
+  const uint16_t* vbase = Vs + (4 * g + (j >> 2)) * Lds<D>::vPitch + 16 * half + 4 * (j & 3);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint16_t* vu = vbase + 16 * u * Lds<D>::vPitch;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      const u32x2 lo = lds_read_tr16(vu + 32 * d);
+      const u32x2 hi = lds_read_tr16(vu + 8 * Lds<D>::vPitch + 32 * d);
+      acc[d] = Mfma<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pk[u], acc[d]);
+    }
   }
 }
 
+// The MFMA phase of a paired-group step: O^T += V^T P^T for the previous
+// tile (HasPV) and S = K Q^T for this one (HasQK), with every LDS read issued
+// one batch ahead of the MFMAs that consume it. In program order:
+//   V^T reads u = 0, 1 | PV u = 0 | reads u = 2 | PV u = 1 | reads u = 3 |
+//   PV u = 2 | K reads 0-3 | PV u = 3 | K reads 4-7 | S MFMAs 0-3 | ...
+// and the sched_group_barrier sequence keeps the compiler from moving the
+// reads back next to their MFMAs (which exposes the LDS latency once per
+// batch) or hoisting them all (which costs registers).
+template <int D, typename T, bool HasPV, bool HasQK>
+__device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const u32x4 (&pk)[4],
+                                                f32x16 (&acc)[D / 32], const uint16_t* Ks,
+                                                const u32x4 (&qr)[D / 16], f32x16 (&sc)[2],
+                                                int lane) {
+  constexpr int KS = D / 16, DT = D / 32;
+  constexpr int NQ = 2 * KS;      // S MFMAs: (half i / KS, k-step i % KS)
+  constexpr int NP = 4 * DT;      // PV MFMAs: (key step u = i / DT, dims tile d = i % DT)
+  constexpr int B = 2;            // MFMAs per batch; each batch's reads go out one batch early
+  const int n = lane & 31, g = lane >> 5;
+  const int j = lane & 15, half = (lane >> 4) & 1;
+  const uint16_t* vbase = Vs + (4 * g + (j >> 2)) * Lds<D>::vPitch + 16 * half + 4 * (j & 3);
+  const uint16_t* kbase = Ks + n * Lds<D>::kPitch + 8 * g;
+  auto vfrag = [&](int i) __attribute__((always_inline)) {
+    const uint16_t* vu = vbase + 16 * (i / DT) * Lds<D>::vPitch + 32 * (i % DT);
+    const u32x2 lo = lds_read_tr16(vu);
+    const u32x2 hi = lds_read_tr16(vu + 8 * Lds<D>::vPitch);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+  auto kfrag = [&](int i) __attribute__((always_inline)) {
+    return *reinterpret_cast<const u32x4*>(kbase + (i / KS) * 32 * Lds<D>::kPitch +
+                                           16 * (i % KS));
+  };
+  // One sequence of A operands: PV MFMAs first (if any), then S MFMAs.
+  constexpr int NA = (HasPV ? NP : 0) + (HasQK ? NQ : 0);
+  auto afrag = [&](int i) __attribute__((always_inline)) {
+    if (HasPV && i < NP) return vfrag(i);
+    return kfrag(i - (HasPV ? NP : 0));
+  };
+  if (HasQK) {
+    sc[0] = f32x16{};
+    sc[1] = f32x16{};
+  }
+  u32x4 fr[2][B];
+#pragma unroll
+  for (int i = 0; i < B; ++i) fr[0][i] = afrag(i);
+#pragma unroll
+  for (int b = 0; b < NA / B; ++b) {
+    if (b + 1 < NA / B) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) fr[(b + 1) & 1][i] = afrag((b + 1) * B + i);
+    }
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int m = b * B + i;
+      if (HasPV && m < NP) {
+        acc[m % DT] = Mfma<T>::run(fr[b & 1][i], pk[m / DT], acc[m % DT]);
+      } else {
+        const int q = m - (HasPV ? NP : 0);
+        sc[q / KS] = Mfma<T>::run(fr[b & 1][i], qr[q % KS], sc[q / KS]);
+      }
+    }
+  }
+  // Schedule: the reads of batch b + 1 before the MFMAs of batch b (two LDS
+  // reads per PV MFMA, one per S MFMA; batches never mix the two kinds).
+  constexpr int NPB = HasPV ? NP / B : 0, NQB = HasQK ? NQ / B : 0;
+  static_assert(NP % B == 0 && NQ % B == 0, "batches must not mix PV and S MFMAs");
+  if (HasPV) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2 * B, 0);
+  else __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
+#pragma unroll
+  for (int b = 0; b < NPB; ++b) {
+    if (b + 1 < NPB) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2 * B, 0);
+    else if (NQB > 0) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
+    __builtin_amdgcn_sched_group_barrier(sg::kMfma, B, 0);
+  }
+#pragma unroll
+  for (int b = 0; b < NQB; ++b) {
+    if (b + 1 < NQB) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
+    __builtin_amdgcn_sched_group_barrier(sg::kMfma, B, 0);
+  }
+}
+
+template <int D, typename T>
+__global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs a) {
+  constexpr int KS = D / 16, DT = D / 32;
+  constexpr int BM = kBMPair;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+
+  const Coord it = locate(a, blockIdx.x, false, 0);
+  const int b = it.b, h = it.h;
+  const int wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);  // 0..7, uniform
+  const int grp = wid >> 2, wave = wid & 3, lane = int(threadIdx.x) & 63;
+  const int g = lane >> 5, n = lane & 31;
+  const int q0 = it.qtile * BM;
+  const int row = grp * 128 + wave * 32 + n;
+  const int qi = q0 + row;
+  const bool qvalid = qi < a.Lq;
+  const bool wave_active = q0 + grp * 128 + wave * 32 < a.Lq;
+  const int cache_len = it.cache_len;
+
+  // Key range of the workgroup (see attn_fwd_kernel).
+  const int kv_min = cache_len + visible_end(a, q0);
+  const int kv_max = cache_len + visible_end(a, min(q0 + BM, a.Lq) - 1);
+  const int n_ct = (cache_len + kBN - 1) / kBN;
+  const int n_tiles = n_ct + (kv_max - cache_len + kBN - 1) / kBN;
+  const int t_begin = int((int64_t(it.split) * n_tiles) / it.n_splits);
+  const int t_end = int((int64_t(it.split + 1) * n_tiles) / it.n_splits);
+  const int nt = t_end - t_begin;
+
+  KvSrc src;
+  src.c_ss2 = int(a.c_ss) * 2;
+  src.k_sl2 = int(a.k_sl) * 2;
+  src.v_sl2 = int(a.v_sl) * 2;
+  src.n_ct = n_ct;
+  {
+    const int rows_c = min(cache_len, kv_max), rows_n = kv_max - cache_len;
+    const int64_t coff = b * a.c_sb + h * a.c_sh;
+    src.kc = make_rsrc(a.ck ? a.ck + coff : a.q, rows_c, src.c_ss2, D);
+    src.vc = make_rsrc(a.cv ? a.cv + coff : a.q, rows_c, src.c_ss2, D);
+    src.kn = make_rsrc(a.k + b * a.k_sb + h * a.k_sh, rows_n, src.k_sl2, D);
+    src.vn = make_rsrc(a.v + b * a.v_sb + h * a.v_sh, rows_n, src.v_sl2, D);
+    src.none = make_rsrc(a.q, 0, 0, D);
+  }
+
+  // Q^T operand (see attn_fwd_kernel): rows past the end load the last row
+  // and are zeroed after the first tile's DMA is out.
+  u32x4 qr[KS];
+  {
+    const uint16_t* qp =
+        a.q + b * a.q_sb + int64_t(min(qi, a.Lq - 1)) * a.q_sl + h * a.q_sh + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+  }
+  auto kbuf = [&](int j) __attribute__((always_inline)) {
+    return smem + (j & 1) * Lds<D>::stage;
+  };
+  auto vbuf = [&](int j) __attribute__((always_inline)) {
+    return smem + (j & 1) * Lds<D>::stage + Lds<D>::kElems;
+  };
+  TileDma<D, T, kPairWaves> dma;
+  dma.init(wid, lane);
+  if (nt > 0) dma.issueK(src, t_begin, wid, kbuf(0));
+  {
+    const uint32_t qmask = qvalid ? ~0u : 0u;
+    const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = (qr[s] & qmask) ^ flip;
+  }
+  const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
+  Softmax sm{-INFINITY, 0.f};
+  const float c = a.scale_log2;
+  f32x16 sc[2];
+  u32x4 pk[4];
+
+  // The first MFMA phase runs its PV on V buffer 1 with P = 0: zero it, so
+  // that whatever an earlier kernel left in LDS (NaN included) contributes
+  // exactly 0.
+  {
+    u32x4* vz = reinterpret_cast<u32x4*>(vbuf(1));
+    for (int i = int(threadIdx.x); i < Lds<D>::vElems / 8; i += 64 * kPairWaves)
+      vz[i] = u32x4{0, 0, 0, 0};
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of K_0
+  __syncthreads();
+
+  // The phase program, global phases p = -1 .. 2 nt (2 nt + 2 barriers for
+  // every wave). Odd phase p = 2m + 1 starts by sending K_{m+2} and V_{m+1}.
+  // Group 0: MFMA phases at odd p (PV_{j-1} and S_j, j = (p + 1) / 2), VALU
+  // phases at even p (softmax of tile p / 2). Group 1: the same one phase
+  // later. Each group runs its own straight-line loop body, so its values
+  // keep their registers from one phase to the next.
+  auto send = [&](int m) __attribute__((always_inline)) {
+    if (m + 2 < nt) dma.issueK(src, t_begin + m + 2, wid, kbuf(m + 2));
+    if (m + 1 < nt) dma.issueV(src, t_begin + m + 1, wid, vbuf(m + 1));
+  };
+  // One straight-line body for every MFMA phase: the first (j = 0) runs PV
+  // with P = 0 (acc unchanged), the last (j = nt) computes an S that is never
+  // used, from a stale but in-bounds K buffer. One extra tile of MFMAs per
+  // work item, against a single register allocation for the phase.
+#pragma unroll
+  for (int u = 0; u < 4; ++u) pk[u] = u32x4{0, 0, 0, 0};
+  auto mfma_phase = [&](int j) __attribute__((always_inline)) {
+    if (wave_active)
+      pair_mfma_phase<D, T, true, true>(vbuf(j - 1), pk, acc, kbuf(j), qr, sc, lane);
+  };
+  auto valu_phase = [&](int j) __attribute__((always_inline)) {
+    if (wave_active) {
+      const int t = t_begin + j;
+      const bool in_cache = t < n_ct;
+      const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
+      const int lim = (in_cache ? cache_len - j0 : my_end - j0) - 4 * g;
+      const bool masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
+      const float mb = softmax_max<D>(sc, acc, sm, c, lim, masked);
+      exp_pack<T>(sc, sm, c, mb, pk);
+    }
+  };
+  // Phase boundary: a bare s_barrier, fenced against compiler reordering of
+  // LDS accesses only. __syncthreads()'s workgroup fence would also wait for
+  // every outstanding DMA piece (they write LDS), putting the full DMA
+  // latency into each phase; instead each wave waits for its own pieces at
+  // the end of the even phase after the odd phase that sent them, one phase
+  // before any wave reads them. LDS reads of a buffer are consumed (their
+  // MFMAs issued) within the phase that reads it, before the boundary after
+  // which the buffer is refilled.
+  auto end_phase = [&](bool even) __attribute__((always_inline)) {
+    if (even) __builtin_amdgcn_s_waitcnt(0);  // pieces sent in the odd phase before
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  if (grp == 0) {
+    send(-1);
+    mfma_phase(0);           // p = -1
+    end_phase(false);
+    for (int j = 0; j < nt; ++j) {
+      valu_phase(j);         // p = 2j
+      end_phase(true);
+      send(j);
+      mfma_phase(j + 1);     // p = 2j + 1
+      end_phase(false);
+    }
+    end_phase(true);         // p = 2 nt
+  } else {
+    send(-1);                // p = -1
+    end_phase(false);
+    mfma_phase(0);           // p = 0
+    end_phase(true);
+    for (int j = 0; j < nt; ++j) {
+      send(j);
+      valu_phase(j);         // p = 2j + 1
+      end_phase(false);
+      mfma_phase(j + 1);     // p = 2j + 2
+      end_phase(true);
+    }
+  }
+
+  const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
+  const float l_tot = sm.l + __shfl_xor(sm.l, 32, 64);
+  if (!qvalid) return;
+  store_result<D, T>(a, it, BM, row, qi, g, acc, l_tot, mref);
+}
+
 template <int D> struct CombineShape {
-  static constexpr int TPR = D / 4;                   // threads per row
-  static constexpr int RPB = 256 / TPR;               // rows per block
-  static constexpr int BPT = (kBM + RPB - 1) / RPB;   // blocks per query tile
+  static constexpr int TPR = D / 4;      // threads per row
+  static constexpr int RPB = 256 / TPR;  // rows per block
 };
 
 // Merge split-KV partials: out = sum_s w_s acc_s / sum_s w_s l_s with
@@ -941,18 +1278,18 @@ template <int D> struct CombineShape {
 template <int D, typename T>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   using CS = CombineShape<D>;
-  const Coord cd = locate(a, blockIdx.x, true, CS::BPT);
+  const Coord cd = locate(a, blockIdx.x, true, a.bm / CS::RPB);
   const int row = cd.split * CS::RPB + threadIdx.x / CS::TPR;
   const int dim = 4 * (threadIdx.x % CS::TPR);
-  const int qi = cd.qtile * kBM + row;
-  if (row >= kBM || qi >= a.Lq) return;
+  const int qi = cd.qtile * a.bm + row;
+  if (qi >= a.Lq) return;
   float2 ml[kMaxSplits];
   u32x2 o[kMaxSplits];
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
     if (s < cd.n_splits) {
-      ml[s] = *reinterpret_cast<const float2*>(a.ws_ml + ((cd.pbase + s) * kBM + row) * 2);
-      o[s] = *reinterpret_cast<const u32x2*>(a.ws_o + ((cd.pbase + s) * kBM + row) * D + dim);
+      ml[s] = *reinterpret_cast<const float2*>(a.ws_ml + ((cd.pbase + s) * a.bm + row) * 2);
+      o[s] = *reinterpret_cast<const u32x2*>(a.ws_o + ((cd.pbase + s) * a.bm + row) * D + dim);
     }
   }
   float mmax = -INFINITY;
@@ -1004,7 +1341,8 @@ int device_cus() {
 
 struct Plan {
   int n_qtiles;
-  int streams;               // 2: decode-shaped (one 8-wave workgroup per CU), 1: prefill
+  int bm;                    // queries per work item
+  int streams;               // 2: dual-stream decode, 1: single stream, 3: paired groups
   int n_seg;                 // 0 = uniform
   int uniform_splits;
   std::vector<int> seg_b, seg_splits, seg_cache, seg_base, comb_base;
@@ -1014,8 +1352,8 @@ struct Plan {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-int64_t combine_bpt(int64_t D) {
-  return D == 128 ? CombineShape<128>::BPT : CombineShape<64>::BPT;
+int64_t combine_bpt(int64_t D, int64_t bm) {
+  return cdiv(bm, D == 128 ? CombineShape<128>::RPB : CombineShape<64>::RPB);
 }
 
 long split_override() {  // DX_ATTN_SPLITS=<n>: tuning override (measurement only)
@@ -1023,11 +1361,15 @@ long split_override() {  // DX_ATTN_SPLITS=<n>: tuning override (measurement onl
   return env ? strtol(env, nullptr, 10) : 0;
 }
 
-long streams_override() {  // DX_ATTN_STREAMS=1|2: tuning override (measurement only)
+// DX_ATTN_STREAMS=1|2|3 (single stream / dual-stream / paired groups):
+// tuning override (measurement only).
+long streams_override() {
   const char* env = getenv("DX_ATTN_STREAMS");
   const long v = env ? strtol(env, nullptr, 10) : 0;
-  return v == 1 || v == 2 ? v : 0;
+  return v >= 1 && v <= 3 ? v : 0;
 }
+
+int bm_of(int streams) { return streams == 3 ? kBMPair : kBM; }
 
 // Split count for `groups` (batch, head, query tile) units of `tiles` key
 // tiles each. Decode-shaped calls (few groups, long key range) get
@@ -1037,19 +1379,27 @@ long streams_override() {  // DX_ATTN_STREAMS=1|2: tuning override (measurement 
 // 192 CUs, finish as fast. Otherwise the split minimising rounds x
 // tiles-per-split (two workgroups per CU) with a small cost per extra split
 // (partials + merge).
-int choose_uniform_splits(int64_t groups, int64_t tiles, int cus, int& streams) {
+int choose_uniform_splits(int64_t units, int64_t Lq, int64_t tiles, int cus, int& streams) {
+  // units: (batch, head) pairs. Decode-shaped at 128 queries per item?
+  const int64_t groups128 = units * cdiv(Lq, kBM);
   int64_t best_s = 1;
-  streams = 1;
-  if (groups * 2 <= cus && tiles >= 4) {
+  if (groups128 * 2 <= cus && tiles >= 4) {
     streams = 2;
-    best_s = std::max<int64_t>(1, std::min<int64_t>({kMaxSplits, (3 * cus) / (4 * groups),
+    best_s = std::max<int64_t>(1, std::min<int64_t>({kMaxSplits, (3 * cus) / (4 * groups128),
                                                       cdiv(tiles, 2)}));
-  } else if (groups < 2 * cus && tiles >= 8) {
-    double best = 1e30;
-    for (int64_t s = 1; s <= kMaxSplits && s <= tiles / 4; ++s) {
-      const double cost = double(cdiv(groups * s, 2 * cus)) * double(cdiv(tiles, s)) +
-                          (s > 1 ? 0.5 * double(s) + 1.0 : 0.0);
-      if (cost < best - 1e-9) { best = cost; best_s = s; }
+  } else {
+    // Paired groups: 256 queries per workgroup, one workgroup per CU; the
+    // split minimising rounds x tiles-per-split, with a small cost per extra
+    // split (partials + merge).
+    streams = 3;
+    const int64_t groups = units * cdiv(Lq, kBMPair);
+    if (groups < 2 * cus && tiles >= 8) {
+      double best = 1e30;
+      for (int64_t s = 1; s <= kMaxSplits && s <= tiles / 4; ++s) {
+        const double cost = double(cdiv(groups * s, cus)) * double(cdiv(tiles, s)) +
+                            (s > 1 ? 0.5 * double(s) + 1.0 : 0.0);
+        if (cost < best - 1e-9) { best = cost; best_s = s; }
+      }
     }
   }
   const long forced = split_override();
@@ -1062,15 +1412,16 @@ int choose_uniform_splits(int64_t groups, int64_t tiles, int cus, int& streams) 
 Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
                const int64_t* cache_lens) {
   Plan p{};
-  p.n_qtiles = int(cdiv(Lq, kBM));
   const int cus = device_cus();
-  const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
   if (!cache_lens) {
     const int64_t tiles = cdiv(cache_len, kBN) + cdiv(Lq, kBN);
-    p.uniform_splits = choose_uniform_splits(B * per_b, tiles, cus, p.streams);
+    p.uniform_splits = choose_uniform_splits(B * H, Lq, tiles, cus, p.streams);
+    p.bm = bm_of(p.streams);
+    p.n_qtiles = int(cdiv(Lq, p.bm));
+    const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
     p.items = B * per_b * p.uniform_splits;
     p.partials = p.uniform_splits > 1 ? p.items : 0;
-    p.comb_blocks = p.uniform_splits > 1 ? B * per_b * combine_bpt(D) : 0;
+    p.comb_blocks = p.uniform_splits > 1 ? B * per_b * combine_bpt(D, p.bm) : 0;
   } else {
     // One segment per sequence, longest first, with splits proportional to
     // its length: within one dual-stream workgroup per CU when that leaves
@@ -1085,9 +1436,13 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
       tiles[i] = cdiv(cache_lens[i], kBN) + cdiv(Lq, kBN);
       total += tiles[i];
     }
+    // Dual-stream decode items (128 queries, one workgroup per CU) when that
+    // leaves <= 8 tiles per split, else paired-group items (256 queries, one
+    // workgroup per CU).
     std::vector<int> splits(B, 1);
-    for (int streams = 2; streams >= 1; --streams) {
-      const double budget = double(cus * (streams == 2 ? 1 : 2)) / double(per_b);
+    for (int streams : {2, 3}) {
+      const int64_t per_b = H * cdiv(Lq, bm_of(streams));
+      const double budget = double(cus) / double(per_b);
       int64_t worst = 0;
       for (int i = 0; i < int(B); ++i) {
         int64_t s = int64_t(budget * double(tiles[i]) / double(std::max<int64_t>(total, 1)));
@@ -1103,6 +1458,9 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
     if (forced >= 1)
       for (int i = 0; i < int(B); ++i)
         splits[i] = int(std::max<int64_t>(1, std::min<int64_t>({forced, kMaxSplits, tiles[i]})));
+    p.bm = bm_of(p.streams);
+    p.n_qtiles = int(cdiv(Lq, p.bm));
+    const int64_t per_b = H * p.n_qtiles;
     p.n_seg = int(B);
     p.seg_base.push_back(0);
     p.comb_base.push_back(0);
@@ -1113,14 +1471,14 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
       p.seg_cache.push_back(int(cache_lens[b]));
       p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[b]));
       p.comb_base.push_back(
-          int(p.comb_base.back() + (splits[b] > 1 ? per_b * combine_bpt(D) : 0)));
+          int(p.comb_base.back() + (splits[b] > 1 ? per_b * combine_bpt(D, p.bm) : 0)));
     }
     p.items = p.seg_base.back();
     p.comb_blocks = p.comb_base.back();
     p.partials = p.items;
   }
   // f16 partial outputs, then fp32 (reference, sum) pairs.
-  p.ws_bytes = p.comb_blocks > 0 ? p.partials * kBM * (D * 2 + 2 * int64_t(sizeof(float))) : 0;
+  p.ws_bytes = p.comb_blocks > 0 ? p.partials * p.bm * (D * 2 + 2 * int64_t(sizeof(float))) : 0;
   return p;
 }
 
@@ -1142,9 +1500,25 @@ hipError_t launch_main(const AttnArgs& a, int64_t items, hipStream_t st) {
 }
 
 template <int D, typename T>
+hipError_t launch_pair(const AttnArgs& a, int64_t items, hipStream_t st) {
+  constexpr int lds = Lds<D>::bytes;
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pair_kernel<D, T>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  });
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((attn_pair_kernel<D, T>), dim3(unsigned(items)), dim3(64 * kPairWaves),
+                     lds, st, a);
+  return hipGetLastError();
+}
+
+template <int D, typename T>
 hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
-  hipError_t e = p.streams == 2 ? launch_main<D, T, 2>(a, p.items, st)
-                                : launch_main<D, T, 1>(a, p.items, st);
+  hipError_t e = p.streams == 2   ? launch_main<D, T, 2>(a, p.items, st)
+                 : p.streams == 3 ? launch_pair<D, T>(a, p.items, st)
+                                  : launch_main<D, T, 1>(a, p.items, st);
   if (e != hipSuccess || p.comb_blocks == 0) return e;
   hipLaunchKernelGGL((attn_combine_kernel<D, T>), dim3(unsigned(p.comb_blocks)), dim3(256), 0,
                      st, a);
@@ -1225,11 +1599,12 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh;
   a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
   a.ws_o = static_cast<uint16_t*>(workspace);
-  a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * kBM * D) : nullptr;
+  a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.bm * D) : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
   a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);
   a.causal = causal != 0;
   a.n_qtiles = p.n_qtiles;
+  a.bm = p.bm;
   // A negative scale enters as a negated q (exact) and |scale|, so the kernel
   // only ever multiplies scores by a non-negative factor.
   a.negate_q = softmax_scale < 0.f;
