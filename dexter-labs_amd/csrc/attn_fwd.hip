@@ -70,6 +70,8 @@ constexpr int kNW = 4;         // waves per workgroup
 constexpr int kBM = 32 * kNW;  // queries per workgroup
 constexpr int kMaxSeg = 64;    // sequences with their own cache length
 constexpr int kMaxSplits = 16;
+constexpr int kPairWaves = 8;  // waves per workgroup of the paired-group kernel
+constexpr int kBMPair = 256;   // its queries per workgroup
 
 struct AttnArgs {
   const uint16_t* q; int64_t q_sb, q_sl, q_sh;
@@ -324,6 +326,16 @@ __device__ __forceinline__ void dma_piece(__amdgpu_buffer_rsrc_t rsrc, const uin
                : "memory");
 }
 
+// The same, to an LDS byte address.
+__device__ __forceinline__ void dma_piece_at(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds,
+                                             uint32_t voff) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(base), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
 // Templated on the element type too, although nothing in it depends on T:
 // with one TileDma<D> shared by the bf16 and f16 kernels, hipcc (ROCm 7.2)
 // silently drops the host-side stub of whichever kernel instantiates it
@@ -380,6 +392,91 @@ struct TileDma {
   }
 };
 
+// LDS of the paired-group kernel: three stages (K tile + V tile each, rows
+// of D elements, no padding). Bank conflicts are avoided by
+// permuting the 16-byte chunks within each row instead of padding, so that
+// the DMA pieces are whole rows and the eight waves get the same number of
+// them:
+//  - K chunk c of row r sits at chunk c ^ kswz(r). The QK^T operand reads of
+//    one instruction take one logical chunk of rows 0..31; kswz gives rows
+//    0..15 (and 16..31) distinct chunks, and rows 0..31 distinct (row parity,
+//    chunk) pairs.
+//  - V chunk c of row r sits at chunk c ^ 4 vswz(r) (only the 64-byte column
+//    group moves, so the 8-byte transposing reads keep their pairs). One
+//    transposing read covers rows r0..r0+3 (lanes 0-31) and r0+4..r0+7
+//    (lanes 32-63) over a 64-byte column group; vswz gives each run of four
+//    rows distinct groups, and the eight rows distinct (row mod 2 (D = 128)
+//    or row mod 4 (D = 64), group) pairs.
+// Both swizzles are invariant under the row offsets the reads add as
+// immediates (32 K rows, 8 and 16 V rows).
+template <int D> struct PairLds {
+  static constexpr int kElems = kBN * D, vElems = kBN * D;
+  static constexpr int stage = kElems + vElems;
+  static constexpr int stages = 3;
+  static constexpr int bytes = stages * stage * 2;
+  __device__ __forceinline__ static int kswz(int r) {
+    return D == 128 ? (r & 15) ^ ((r >> 4) & 1) : ((r >> 2) ^ (4 * ((r >> 1) & 1))) & 7;
+  }
+  __device__ __forceinline__ static int vswz(int r) {
+    return D == 128 ? (r & 3) ^ ((r >> 2) & 1) : ((r >> 1) ^ (r >> 2)) & 1;
+  }
+};
+
+// Fixed DMA slots of the paired-group kernel. A K (or V) tile is PK pieces of
+// RPP whole rows; piece p of each goes to wave p % 8, so every wave issues
+// exactly NK K pieces and NK V pieces per tile step, none of them behind a
+// branch. Lane l of a piece fills physical chunk l % CR of row l / CR, so it
+// fetches the logical chunk the swizzle puts there. Slots of steps outside
+// the work item still issue (and write zeros). The count of a wave's pieces in flight is therefore a
+// compile-time constant, which lets a wave wait for one step's pieces while
+// the next step's are still flying.
+template <int D, typename T>
+struct PairDma {
+  static constexpr int CR = D / 8;             // 16-byte chunks per row
+  static constexpr int RPP = 64 / CR;          // rows per piece
+  static constexpr int PK = kBN / RPP;         // pieces per K (or V) tile
+  static constexpr int NK = PK / kPairWaves;   // K (and V) slots per wave
+  static constexpr int NP = 2 * NK;            // slots per wave and step
+  static_assert(PK % kPairWaves == 0, "tile pieces must deal evenly over the waves");
+  int pc[NP];  // this lane's (row << 16) | byte column per slot
+
+  __device__ __forceinline__ void init(int wid, int lane) {
+#pragma unroll
+    for (int m = 0; m < NP; ++m) {
+      const int r = (wid + kPairWaves * (m % NK)) * RPP + lane / CR, x = lane % CR;
+      const int c = m < NK ? x ^ PairLds<D>::kswz(r) : x ^ (4 * PairLds<D>::vswz(r));
+      pc[m] = (r << 16) | (c * 16);
+    }
+  }
+  // Slot m (K slots first): its piece of K_{jk} or of V_{jv}, steps relative
+  // to the work item's first tile (>= -1), stages rotating over the three;
+  // lds is the LDS byte address of stage 0. A step outside [0, nt) reads
+  // past the end of its descriptor and fills its stage with zeros: that
+  // stage is free at the time (as for a live step), and step -1's V stage is
+  // the one the first MFMA phase must find zeroed anyway.
+  __device__ __forceinline__ void issue(int m, const KvSrc& src, uint32_t lds, int t_begin,
+                                        int nt, int jk, int jv, int wid) const {
+    const bool is_k = m < NK;  // known at compile time in every caller
+    const int jt = is_k ? jk : jv;
+    const bool live = jt >= 0 && jt < nt;
+    const int t = t_begin + jt;
+    const bool in_cache = t < src.n_ct;
+    const __amdgpu_buffer_rsrc_t xc = is_k ? src.kc : src.vc, xn = is_k ? src.kn : src.vn;
+    const __amdgpu_buffer_rsrc_t r = in_cache ? xc : xn;
+    const int stride = in_cache ? src.c_ss2 : (is_k ? src.k_sl2 : src.v_sl2);
+    const int row0 = (in_cache ? t : t - src.n_ct) * kBN;
+    const int p = wid + kPairWaves * (m % NK);
+    const int at = ((jt + 3) % 3) * PairLds<D>::stage + (is_k ? 0 : PairLds<D>::kElems) + p * 512;
+    // Past the end by setting bit 31 (descriptors hold < 2^31 bytes), not by a
+    // select: the compiler turns a select of vector values on a uniform
+    // condition into a branch, which would cut the MFMA phase's schedule.
+    const uint32_t past = live ? 0u : 0x80000000u;
+    const uint32_t voff =
+        (uint32_t(row0 + (pc[m] >> 16)) * uint32_t(stride) + uint32_t(pc[m] & 0xffff)) | past;
+    dma_piece_at(r, lds + 2 * at, voff);
+  }
+};
+
 // Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each group of 16
 // lanes, lane i receives element i % 4 of the 8-byte chunks addressed by
 // lanes 4e + i / 4, e = 0..3 of its group.
@@ -388,6 +485,21 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
   const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_v4i16*)((__attribute__((address_space(3))) uint16_t*)(p)));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// LDS accesses by byte address (for the swizzled layout, whose addresses are
+// built with XOR).
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(uintptr_t((__attribute__((address_space(3))) const void*)(p)));
+}
+__device__ __forceinline__ u32x4 lds_read_b128_at(uint32_t addr) {
+  return *reinterpret_cast<const lds_u32x4*>(addr);
+}
+__device__ __forceinline__ u32x2 lds_read_tr16_at(uint32_t addr) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_v4i16*>(addr));
   return __builtin_bit_cast(u32x2, r);
 }
 
@@ -494,6 +606,19 @@ __device__ __forceinline__ bool key_hidden(int kt, int r, int lim) {
   return 32 * kt + 8 * (r / 4) + (r % 4) >= lim;
 }
 
+// Combine lanes i and i ^ 32 (v_permlane32_swap: a VALU exchange of the two
+// wave halves, with no trip through the LDS queue as ds_bpermute takes).
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Returns the exponent base (max in log2 units, 0 while nothing is visible).
 template <int D>
 __device__ __forceinline__ float softmax_max(f32x16 (&s)[2], f32x16 (&acc)[D / 32],
@@ -516,7 +641,7 @@ __device__ __forceinline__ float softmax_max(f32x16 (&s)[2], f32x16 (&acc)[D / 3
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  tmax = xor32_max(tmax);
   const float m_new = fmaxf(sm.m, tmax);
   // Lazy rescale (wave-uniform branch): only when some lane's max grew by
   // more than 2^8. Before anything is accumulated (m = -inf on every lane)
@@ -948,7 +1073,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     mref = mm;
   }
 
-  const float l_tot = sm.l + __shfl_xor(sm.l, 32, 64);
+  const float l_tot = xor32_sum(sm.l);
   if (!qvalid) return;
   store_result<D, T>(a, it, kBM, wave * 32 + n, qi, g, acc, l_tot, mref);
 }
@@ -975,8 +1100,6 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 // buffer, free since then too), and waits for them at the end of phase 2m+2:
 // two phases of latency cover, nothing overwritten while read.
 // ---------------------------------------------------------------------------
-constexpr int kPairWaves = 8;
-constexpr int kBMPair = 256;
 
 // P = exp2(S c - mb) packed to 16-bit pairs in MFMA B-operand order (pk[u][e]:
 // keys 8 (u % 2) + 2 e, +1 of half u / 2) and the row sum over the packed
@@ -1022,47 +1145,58 @@ __device__ __forceinline__ void pv_packed(const uint16_t* Vs, const u32x4 (&pk)[
   }
 }
 
-// The MFMA phase of a paired-group step: O^T += V^T P^T for the previous
-// tile (HasPV) and S = K Q^T for this one (HasQK), with every LDS read issued
-// one batch ahead of the MFMAs that consume it. In program order:
-//   V^T reads u = 0, 1 | PV u = 0 | reads u = 2 | PV u = 1 | reads u = 3 |
-//   PV u = 2 | K reads 0-3 | PV u = 3 | K reads 4-7 | S MFMAs 0-3 | ...
-// and the sched_group_barrier sequence keeps the compiler from moving the
-// reads back next to their MFMAs (which exposes the LDS latency once per
-// batch) or hoisting them all (which costs registers).
-template <int D, typename T, bool HasPV, bool HasQK>
-__device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const u32x4 (&pk)[4],
-                                                f32x16 (&acc)[D / 32], const uint16_t* Ks,
-                                                const u32x4 (&qr)[D / 16], f32x16 (&sc)[2],
-                                                int lane) {
+// The MFMA phase of a paired-group step: S = K Q^T for this tile, then
+// O^T += V^T P^T for the previous one. While the S MFMAs run, the wave packs
+// the previous tile's exponentials (pf, fp32) into MFMA operands (pk) and
+// adds their row sums to l, so that this vector work, which has no MFMA
+// dependency, fills the issue slots of the MFMA phase instead of lengthening
+// the VALU phase. Every LDS read is issued one batch ahead of the MFMAs that
+// consume it; the sched_group_barrier sequence keeps the compiler from
+// moving the reads back next to their MFMAs (which exposes the LDS latency
+// once per batch) or hoisting them all (which costs registers). NSend DMA
+// slots (send(m)) are spread between the batches.
+template <int D, typename T, int NSend, class Send>
+__device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16 (&pf)[2],
+                                                float& l, f32x16 (&acc)[D / 32],
+                                                const uint16_t* Ks, const u32x4 (&qr)[D / 16],
+                                                f32x16 (&sc)[2], int lane, const Send& send) {
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int NQ = 2 * KS;      // S MFMAs: (half i / KS, k-step i % KS)
   constexpr int NP = 4 * DT;      // PV MFMAs: (key step u = i / DT, dims tile d = i % DT)
+  constexpr int NA = NQ + NP;
   constexpr int B = 2;            // MFMAs per batch; each batch's reads go out one batch early
+  constexpr int NQB = NQ / B, NPB = NP / B;
+  static_assert(NQ % B == 0 && NP % B == 0, "batches must not mix PV and S MFMAs");
+  static_assert(16 % NQB == 0, "the packing must split evenly over the S batches");
+  using L = PairLds<D>;
+  constexpr int RB = 2 * D;       // bytes per row
   const int n = lane & 31, g = lane >> 5;
   const int j = lane & 15, half = (lane >> 4) & 1;
-  const uint16_t* vbase = Vs + (4 * g + (j >> 2)) * Lds<D>::vPitch + 16 * half + 4 * (j & 3);
-  const uint16_t* kbase = Ks + n * Lds<D>::kPitch + 8 * g;
+  // V^T operand: rows r0 (+ 8, + 16 u), bytes 32 half + 8 (j % 4) of 64-byte
+  // column group d, which sits at group d ^ vswz(r0).
+  const int r0 = 4 * g + (j >> 2);
+  const uint32_t vaddr = lds_addr(Vs) + r0 * RB + 32 * half + 8 * (j & 3) + 64 * L::vswz(r0);
+  // S operand: row n (+ 32), logical chunk 2 s + g at chunk (2 s + g) ^ kswz(n).
+  const uint32_t kaddr = lds_addr(Ks) + n * RB + 16 * (g ^ L::kswz(n));
   auto vfrag = [&](int i) __attribute__((always_inline)) {
-    const uint16_t* vu = vbase + 16 * (i / DT) * Lds<D>::vPitch + 32 * (i % DT);
-    const u32x2 lo = lds_read_tr16(vu);
-    const u32x2 hi = lds_read_tr16(vu + 8 * Lds<D>::vPitch);
+    const uint32_t vu = (vaddr ^ (64 * (i % DT))) + 16 * (i / DT) * RB;
+    const u32x2 lo = lds_read_tr16_at(vu);
+    const u32x2 hi = lds_read_tr16_at(vu + 8 * RB);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
   auto kfrag = [&](int i) __attribute__((always_inline)) {
-    return *reinterpret_cast<const u32x4*>(kbase + (i / KS) * 32 * Lds<D>::kPitch +
-                                           16 * (i % KS));
+    return lds_read_b128_at((kaddr ^ (32 * (i % KS))) + (i / KS) * 32 * RB);
   };
-  // One sequence of A operands: PV MFMAs first (if any), then S MFMAs.
-  constexpr int NA = (HasPV ? NP : 0) + (HasQK ? NQ : 0);
+  // One sequence of A operands: S MFMAs first, then PV MFMAs.
   auto afrag = [&](int i) __attribute__((always_inline)) {
-    if (HasPV && i < NP) return vfrag(i);
-    return kfrag(i - (HasPV ? NP : 0));
+    return i < NQ ? kfrag(i) : vfrag(i - NQ);
   };
-  if (HasQK) {
-    sc[0] = f32x16{};
-    sc[1] = f32x16{};
-  }
+  // pk[u][e]: keys 8 (u % 2) + 2 e, +1 of half u / 2 (MFMA B-operand order).
+  u32x4 pk[4];
+  float part[2] = {0.f, 0.f};
+  constexpr int PPB = 16 / NQB;   // packed pairs per S batch
+  sc[0] = f32x16{};
+  sc[1] = f32x16{};
   u32x4 fr[2][B];
 #pragma unroll
   for (int i = 0; i < B; ++i) fr[0][i] = afrag(i);
@@ -1075,29 +1209,41 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const u32x4 
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const int m = b * B + i;
-      if (HasPV && m < NP) {
-        acc[m % DT] = Mfma<T>::run(fr[b & 1][i], pk[m / DT], acc[m % DT]);
+      if (m < NQ) {
+        sc[m / KS] = Mfma<T>::run(fr[b & 1][i], qr[m % KS], sc[m / KS]);
       } else {
-        const int q = m - (HasPV ? NP : 0);
-        sc[q / KS] = Mfma<T>::run(fr[b & 1][i], qr[q % KS], sc[q / KS]);
+        const int q = m - NQ;
+        acc[q % DT] = Mfma<T>::run(fr[b & 1][i], pk[q / DT], acc[q % DT]);
       }
     }
-  }
-  // Schedule: the reads of batch b + 1 before the MFMAs of batch b (two LDS
-  // reads per PV MFMA, one per S MFMA; batches never mix the two kinds).
-  constexpr int NPB = HasPV ? NP / B : 0, NQB = HasQK ? NQ / B : 0;
-  static_assert(NP % B == 0 && NQ % B == 0, "batches must not mix PV and S MFMAs");
-  if (HasPV) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2 * B, 0);
-  else __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
+    if (b < NQB) {
 #pragma unroll
-  for (int b = 0; b < NPB; ++b) {
-    if (b + 1 < NPB) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2 * B, 0);
-    else if (NQB > 0) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
-    __builtin_amdgcn_sched_group_barrier(sg::kMfma, B, 0);
+      for (int x = 0; x < PPB; ++x) {
+        const int w = b * PPB + x, u = w / 4, e = w % 4;
+        const uint32_t pp = Mfma<T>::pack(pf[u / 2][8 * (u % 2) + 2 * e],
+                                          pf[u / 2][8 * (u % 2) + 2 * e + 1]);
+        pk[u][e] = pp;
+        part[e & 1] = Mfma<T>::sum2(pp, part[e & 1]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NSend; ++m)
+      if (b == 1 + m * (NA / B) / (NSend > 0 ? NSend : 1)) send(m);
   }
+  l += part[0] + part[1];
+  // Schedule: batch b's MFMAs after the reads of batch b + 1 (two LDS reads
+  // per PV MFMA, one per S MFMA); the packing's vector instructions (two per
+  // pair) after each S batch's MFMAs.
+  __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
 #pragma unroll
   for (int b = 0; b < NQB; ++b) {
     if (b + 1 < NQB) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
+    else __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2 * B, 0);
+    __builtin_amdgcn_sched_group_barrier(sg::kMfma, B, 0);
+  }
+#pragma unroll
+  for (int b = 0; b < NPB; ++b) {
+    if (b + 1 < NPB) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2 * B, 0);
     __builtin_amdgcn_sched_group_barrier(sg::kMfma, B, 0);
   }
 }
@@ -1153,15 +1299,19 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 #pragma unroll
     for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
   }
+  // Three stages; step j (tile t_begin + j) uses stage j % 3 (j >= -1).
   auto kbuf = [&](int j) __attribute__((always_inline)) {
-    return smem + (j & 1) * Lds<D>::stage;
+    return smem + ((j + 3) % 3) * PairLds<D>::stage;
   };
   auto vbuf = [&](int j) __attribute__((always_inline)) {
-    return smem + (j & 1) * Lds<D>::stage + Lds<D>::kElems;
+    return smem + ((j + 3) % 3) * PairLds<D>::stage + PairLds<D>::kElems;
   };
-  TileDma<D, T, kPairWaves> dma;
+  using Dma = PairDma<D, T>;
+  const uint32_t smem_b = lds_addr(smem);
+  Dma dma;
   dma.init(wid, lane);
-  if (nt > 0) dma.issueK(src, t_begin, wid, kbuf(0));
+#pragma unroll
+  for (int m = 0; m < Dma::NP; ++m) dma.issue(m, src, smem_b, t_begin, nt, 0, -1, wid);
   {
     const uint32_t qmask = qvalid ? ~0u : 0u;
     const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
@@ -1176,92 +1326,116 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   Softmax sm{-INFINITY, 0.f};
   const float c = a.scale_log2;
   f32x16 sc[2];
-  u32x4 pk[4];
+  f32x16 pf[2];  // exponentials of the last tile, packed in the next MFMA phase
 
-  // The first MFMA phase runs its PV on V buffer 1 with P = 0: zero it, so
-  // that whatever an earlier kernel left in LDS (NaN included) contributes
-  // exactly 0.
-  {
-    u32x4* vz = reinterpret_cast<u32x4*>(vbuf(1));
-    for (int i = int(threadIdx.x); i < Lds<D>::vElems / 8; i += 64 * kPairWaves)
-      vz[i] = u32x4{0, 0, 0, 0};
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of K_0
+  // The first MFMA phase runs its PV on V stage -1 with P = 0. Step -1's V
+  // slots above filled that stage with zeros, so whatever an earlier kernel
+  // left in LDS (NaN included) contributes exactly 0.
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of K_0 and of V stage -1
   __syncthreads();
 
   // The phase program, global phases p = -1 .. 2 nt (2 nt + 2 barriers for
-  // every wave). Odd phase p = 2m + 1 starts by sending K_{m+2} and V_{m+1}.
-  // Group 0: MFMA phases at odd p (PV_{j-1} and S_j, j = (p + 1) / 2), VALU
-  // phases at even p (softmax of tile p / 2). Group 1: the same one phase
+  // every wave). Group 0 runs MFMA phase j (PV_{j-1} and S_j) at p = 2j - 1
+  // and the VALU phase of tile j at p = 2j; group 1 runs each one phase
   // later. Each group runs its own straight-line loop body, so its values
   // keep their registers from one phase to the next.
-  auto send = [&](int m) __attribute__((always_inline)) {
-    if (m + 2 < nt) dma.issueK(src, t_begin + m + 2, wid, kbuf(m + 2));
-    if (m + 1 < nt) dma.issueV(src, t_begin + m + 1, wid, vbuf(m + 1));
+  //
+  // DMA: during VALU phase j every wave sends its slots of step j
+  // (K_{j+2}, V_{j+1}), spread between the exponentials. K_{j+2}'s stage last held K_{j-1}, read in MFMA
+  // phases j-1 (p <= 2j - 2); V_{j+1}'s held V_{j-2}, read in the same
+  // phases: both free by p = 2j, group 0's send of step j. Step j's pieces
+  // are first read at p = 2j + 3; every wave has them waited for by the
+  // barrier ending p = 2j + 2. Group 0 sent step j + 1 at p = 2j + 2 and
+  // keeps those NP pieces in flight; group 1 (sends at odd p) has nothing
+  // newer and waits for all.
+  auto send = [&](int j) __attribute__((always_inline)) {
+    return [&, j](int m) __attribute__((always_inline)) {
+      dma.issue(m, src, smem_b, t_begin, nt, j + 2, j + 1, wid);
+    };
   };
   // One straight-line body for every MFMA phase: the first (j = 0) runs PV
   // with P = 0 (acc unchanged), the last (j = nt) computes an S that is never
   // used, from a stale but in-bounds K buffer. One extra tile of MFMAs per
   // work item, against a single register allocation for the phase.
 #pragma unroll
-  for (int u = 0; u < 4; ++u) pk[u] = u32x4{0, 0, 0, 0};
+  for (int kt = 0; kt < 2; ++kt) pf[kt] = f32x16{};
+  // The wave in its MFMA phase issues ahead of its SIMD partner (raised
+  // priority): an MFMA it cannot issue idles the matrix pipe, while the
+  // partner's vector work fills whatever issue cycles are left.
   auto mfma_phase = [&](int j) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_setprio(1);
     if (wave_active)
-      pair_mfma_phase<D, T, true, true>(vbuf(j - 1), pk, acc, kbuf(j), qr, sc, lane);
+      pair_mfma_phase<D, T, 0>(vbuf(j - 1), pf, sm.l, acc, kbuf(j), qr, sc, lane, send(j));
+    __builtin_amdgcn_s_setprio(0);
   };
+  static_assert(Dma::NP == 4 || Dma::NP == 2, "DMA slots are spread over the 32 exponentials");
   auto valu_phase = [&](int j) __attribute__((always_inline)) {
-    if (wave_active) {
+    if (!wave_active) {
+#pragma unroll
+      for (int m = 0; m < Dma::NP; ++m) send(j)(m);
+    } else {
       const int t = t_begin + j;
       const bool in_cache = t < n_ct;
       const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
       const int lim = (in_cache ? cache_len - j0 : my_end - j0) - 4 * g;
       const bool masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
       const float mb = softmax_max<D>(sc, acc, sm, c, lim, masked);
-      exp_pack<T>(sc, sm, c, mb, pk);
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          pf[kt][r] = fast_exp2(__builtin_fmaf(sc[kt][r], c, -mb));
+          constexpr int every = 32 / Dma::NP;
+          if ((16 * kt + r) % every == every - 1) send(j)((16 * kt + r) / every);
+        }
     }
   };
   // Phase boundary: a bare s_barrier, fenced against compiler reordering of
   // LDS accesses only. __syncthreads()'s workgroup fence would also wait for
-  // every outstanding DMA piece (they write LDS), putting the full DMA
-  // latency into each phase; instead each wave waits for its own pieces at
-  // the end of the even phase after the odd phase that sent them, one phase
-  // before any wave reads them. LDS reads of a buffer are consumed (their
-  // MFMAs issued) within the phase that reads it, before the boundary after
-  // which the buffer is refilled.
+  // every outstanding DMA piece (they write LDS); instead, at the end of an
+  // even phase, a wave waits for the pieces it must have landed (loads
+  // complete in order) and for its LDS reads.
+  constexpr int kWaitOld = (Dma::NP & 15) | ((Dma::NP >> 4) << 14) | (7 << 4);  // vmcnt(NP) lgkmcnt(0)
   auto end_phase = [&](bool even) __attribute__((always_inline)) {
-    if (even) __builtin_amdgcn_s_waitcnt(0);  // pieces sent in the odd phase before
+    if (even) {
+      if (grp == 0) __builtin_amdgcn_s_waitcnt(kWaitOld);
+      else __builtin_amdgcn_s_waitcnt(0);
+    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
   if (grp == 0) {
-    send(-1);
+#pragma unroll
+    for (int m = 0; m < Dma::NP; ++m) send(-1)(m);
     mfma_phase(0);           // p = -1
     end_phase(false);
     for (int j = 0; j < nt; ++j) {
       valu_phase(j);         // p = 2j
       end_phase(true);
-      send(j);
       mfma_phase(j + 1);     // p = 2j + 1
       end_phase(false);
     }
     end_phase(true);         // p = 2 nt
   } else {
-    send(-1);                // p = -1
-    end_phase(false);
+#pragma unroll
+    for (int m = 0; m < Dma::NP; ++m) send(-1)(m);
+    end_phase(false);        // p = -1
     mfma_phase(0);           // p = 0
     end_phase(true);
     for (int j = 0; j < nt; ++j) {
-      send(j);
       valu_phase(j);         // p = 2j + 1
       end_phase(false);
       mfma_phase(j + 1);     // p = 2j + 2
       end_phase(true);
     }
   }
+  // The last sends (steps past the end, zeros) must land before the
+  // workgroup's LDS is handed to the next one.
+  __builtin_amdgcn_s_waitcnt(0);
 
   const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
-  const float l_tot = sm.l + __shfl_xor(sm.l, 32, 64);
+  const float l_tot = xor32_sum(sm.l);
   if (!qvalid) return;
   store_result<D, T>(a, it, BM, row, qi, g, acc, l_tot, mref);
 }
@@ -1501,7 +1675,7 @@ hipError_t launch_main(const AttnArgs& a, int64_t items, hipStream_t st) {
 
 template <int D, typename T>
 hipError_t launch_pair(const AttnArgs& a, int64_t items, hipStream_t st) {
-  constexpr int lds = Lds<D>::bytes;
+  constexpr int lds = PairLds<D>::bytes;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
