@@ -438,22 +438,30 @@ struct PairDma {
   static constexpr int NK = PK / kPairWaves;   // K (and V) slots per wave
   static constexpr int NP = 2 * NK;            // slots per wave and step
   static_assert(PK % kPairWaves == 0, "tile pieces must deal evenly over the waves");
-  int pc[NP];  // this lane's (row << 16) | byte column per slot
+  // This lane's byte offset per slot, within its tile, for the new-key row
+  // stride (on), and what to add for the cache's row stride instead (dc).
+  uint32_t on[NP], dc[NP];
 
-  __device__ __forceinline__ void init(int wid, int lane) {
+  __device__ __forceinline__ void init(int wid, int lane, const KvSrc& src) {
 #pragma unroll
     for (int m = 0; m < NP; ++m) {
       const int r = (wid + kPairWaves * (m % NK)) * RPP + lane / CR, x = lane % CR;
       const int c = m < NK ? x ^ PairLds<D>::kswz(r) : x ^ (4 * PairLds<D>::vswz(r));
-      pc[m] = (r << 16) | (c * 16);
+      const uint32_t sn = uint32_t(m < NK ? src.k_sl2 : src.v_sl2);
+      on[m] = uint32_t(r) * sn + uint32_t(c * 16);
+      dc[m] = uint32_t(r) * (uint32_t(src.c_ss2) - sn);
     }
   }
   // Slot m (K slots first): its piece of K_{jk} or of V_{jv}, steps relative
   // to the work item's first tile (>= -1), stages rotating over the three;
   // lds is the LDS byte address of stage 0. A step outside [0, nt) reads
-  // past the end of its descriptor and fills its stage with zeros: that
-  // stage is free at the time (as for a live step), and step -1's V stage is
-  // the one the first MFMA phase must find zeroed anyway.
+  // past the end of its descriptor (bit 31 set: descriptors hold < 2^31
+  // bytes) and fills its stage with zeros: that stage is free at the time
+  // (as for a live step), and step -1's V stage is the one the first MFMA
+  // phase must find zeroed anyway. Two vector instructions per piece; the
+  // rest is scalar. No selects of vector values on the step's (uniform)
+  // conditions: the compiler turns those into branches, which would cut the
+  // phase's schedule.
   __device__ __forceinline__ void issue(int m, const KvSrc& src, uint32_t lds, int t_begin,
                                         int nt, int jk, int jv, int wid) const {
     const bool is_k = m < NK;  // known at compile time in every caller
@@ -465,15 +473,11 @@ struct PairDma {
     const __amdgpu_buffer_rsrc_t r = in_cache ? xc : xn;
     const int stride = in_cache ? src.c_ss2 : (is_k ? src.k_sl2 : src.v_sl2);
     const int row0 = (in_cache ? t : t - src.n_ct) * kBN;
+    const uint32_t base = live ? uint32_t(row0) * uint32_t(stride) : 0x80000000u;
+    const uint32_t cmask = in_cache ? ~0u : 0u;
     const int p = wid + kPairWaves * (m % NK);
     const int at = ((jt + 3) % 3) * PairLds<D>::stage + (is_k ? 0 : PairLds<D>::kElems) + p * 512;
-    // Past the end by setting bit 31 (descriptors hold < 2^31 bytes), not by a
-    // select: the compiler turns a select of vector values on a uniform
-    // condition into a branch, which would cut the MFMA phase's schedule.
-    const uint32_t past = live ? 0u : 0x80000000u;
-    const uint32_t voff =
-        (uint32_t(row0 + (pc[m] >> 16)) * uint32_t(stride) + uint32_t(pc[m] & 0xffff)) | past;
-    dma_piece_at(r, lds + 2 * at, voff);
+    dma_piece_at(r, lds + 2 * at, on[m] + (dc[m] & cmask) + base);
   }
 };
 
@@ -635,13 +639,14 @@ __device__ __forceinline__ float softmax_max(f32x16 (&s)[2], f32x16 (&acc)[D / 3
       for (int r = 0; r < 16; ++r)
         if (key_hidden(kt, r, l)) s[kt][r] = -INFINITY;
   }
-  // Row max over the visible scores (raw units; c >= 0 keeps the order).
-  float tmax = -INFINITY;
+  // Row max over the visible scores (raw units; c >= 0 keeps the order), as
+  // four independent chains so the dependent max latency overlaps.
+  float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kt][r]);
-  tmax = xor32_max(tmax);
+    for (int r = 0; r < 16; ++r) tm[r % 4] = fmaxf(tm[r % 4], s[kt][r]);
+  const float tmax = xor32_max(fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3])));
   const float m_new = fmaxf(sm.m, tmax);
   // Lazy rescale (wave-uniform branch): only when some lane's max grew by
   // more than 2^8. Before anything is accumulated (m = -inf on every lane)
@@ -1161,7 +1166,7 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16
                                                 const uint16_t* Ks, const u32x4 (&qr)[D / 16],
                                                 f32x16 (&sc)[2], int lane, const Send& send) {
   constexpr int KS = D / 16, DT = D / 32;
-  constexpr int NQ = 2 * KS;      // S MFMAs: (half i / KS, k-step i % KS)
+  constexpr int NQ = 2 * KS;      // S MFMAs: (half i % 2, k-step i / 2): two interleaved chains
   constexpr int NP = 4 * DT;      // PV MFMAs: (key step u = i / DT, dims tile d = i % DT)
   constexpr int NA = NQ + NP;
   constexpr int B = 2;            // MFMAs per batch; each batch's reads go out one batch early
@@ -1185,7 +1190,7 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
   auto kfrag = [&](int i) __attribute__((always_inline)) {
-    return lds_read_b128_at((kaddr ^ (32 * (i % KS))) + (i / KS) * 32 * RB);
+    return lds_read_b128_at((kaddr ^ (32 * (i / 2))) + (i % 2) * 32 * RB);
   };
   // One sequence of A operands: S MFMAs first, then PV MFMAs.
   auto afrag = [&](int i) __attribute__((always_inline)) {
@@ -1193,7 +1198,7 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16
   };
   // pk[u][e]: keys 8 (u % 2) + 2 e, +1 of half u / 2 (MFMA B-operand order).
   u32x4 pk[4];
-  float part[2] = {0.f, 0.f};
+  float part[2] = {0.f, 0.f};  // same pairing as the other kernels: identical sums
   constexpr int PPB = 16 / NQB;   // packed pairs per S batch
   sc[0] = f32x16{};
   sc[1] = f32x16{};
@@ -1210,7 +1215,7 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16
     for (int i = 0; i < B; ++i) {
       const int m = b * B + i;
       if (m < NQ) {
-        sc[m / KS] = Mfma<T>::run(fr[b & 1][i], qr[m % KS], sc[m / KS]);
+        sc[m % 2] = Mfma<T>::run(fr[b & 1][i], qr[m / 2], sc[m % 2]);
       } else {
         const int q = m - NQ;
         acc[q % DT] = Mfma<T>::run(fr[b & 1][i], pk[q / DT], acc[q % DT]);
@@ -1309,7 +1314,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   using Dma = PairDma<D, T>;
   const uint32_t smem_b = lds_addr(smem);
   Dma dma;
-  dma.init(wid, lane);
+  dma.init(wid, lane, src);
 #pragma unroll
   for (int m = 0; m < Dma::NP; ++m) dma.issue(m, src, smem_b, t_begin, nt, 0, -1, wid);
   {
