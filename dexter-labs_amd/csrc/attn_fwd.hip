@@ -410,10 +410,14 @@ struct TileDma {
 // Both swizzles are invariant under the row offsets the reads add as
 // immediates (32 K rows, 8 and 16 V rows).
 template <int D> struct PairLds {
-  static constexpr int kElems = kBN * D, vElems = kBN * D;
-  static constexpr int stage = kElems + vElems;
+  static constexpr int kElems = kBN * D, vElems = kBN * D;  // one tile each
   static constexpr int stages = 3;
-  static constexpr int bytes = stages * stage * 2;
+  // Element offsets of stage s's K and V tiles: the three K tiles, then the
+  // three V tiles, so that every read offset fits the LDS instructions'
+  // 16-bit immediate (given a per-lane base that includes the V region's).
+  static constexpr int kstage(int s) { return s * kElems; }
+  static constexpr int vstage(int s) { return stages * kElems + s * vElems; }
+  static constexpr int bytes = stages * (kElems + vElems) * 2;
   __device__ __forceinline__ static int kswz(int r) {
     return D == 128 ? (r & 15) ^ ((r >> 4) & 1) : ((r >> 2) ^ (4 * ((r >> 1) & 1))) & 7;
   }
@@ -452,9 +456,10 @@ struct PairDma {
       dc[m] = uint32_t(r) * (uint32_t(src.c_ss2) - sn);
     }
   }
-  // Slot m (K slots first): its piece of K_{jk} or of V_{jv}, steps relative
-  // to the work item's first tile (>= -1), stages rotating over the three;
-  // lds is the LDS byte address of stage 0. A step outside [0, nt) reads
+  // Slot m (K slots first): its piece of K_{jk} into K stage kst, or of
+  // V_{jv} into V stage vst (steps relative to the work item's first tile,
+  // >= -1; step j uses stage j mod 3); lds is the LDS byte address of the
+  // tile area. A step outside [0, nt) reads
   // past the end of its descriptor (bit 31 set: descriptors hold < 2^31
   // bytes) and fills its stage with zeros: that stage is free at the time
   // (as for a live step), and step -1's V stage is the one the first MFMA
@@ -463,7 +468,8 @@ struct PairDma {
   // conditions: the compiler turns those into branches, which would cut the
   // phase's schedule.
   __device__ __forceinline__ void issue(int m, const KvSrc& src, uint32_t lds, int t_begin,
-                                        int nt, int jk, int jv, int wid) const {
+                                        int nt, int jk, int jv, int kst, int vst,
+                                        int wid) const {
     const bool is_k = m < NK;  // known at compile time in every caller
     const int jt = is_k ? jk : jv;
     const bool live = jt >= 0 && jt < nt;
@@ -476,7 +482,7 @@ struct PairDma {
     const uint32_t base = live ? uint32_t(row0) * uint32_t(stride) : 0x80000000u;
     const uint32_t cmask = in_cache ? ~0u : 0u;
     const int p = wid + kPairWaves * (m % NK);
-    const int at = ((jt + 3) % 3) * PairLds<D>::stage + (is_k ? 0 : PairLds<D>::kElems) + p * 512;
+    const int at = (is_k ? PairLds<D>::kstage(kst) : PairLds<D>::vstage(vst)) + p * 512;
     dma_piece_at(r, lds + 2 * at, on[m] + (dc[m] & cmask) + base);
   }
 };
@@ -1150,22 +1156,47 @@ __device__ __forceinline__ void pv_packed(const uint16_t* Vs, const u32x4 (&pk)[
   }
 }
 
-// The MFMA phase of a paired-group step: S = K Q^T for this tile, then
-// O^T += V^T P^T for the previous one. While the S MFMAs run, the wave packs
-// the previous tile's exponentials (pf, fp32) into MFMA operands (pk) and
-// adds their row sums to l, so that this vector work, which has no MFMA
-// dependency, fills the issue slots of the MFMA phase instead of lengthening
-// the VALU phase. Every LDS read is issued one batch ahead of the MFMAs that
-// consume it; the sched_group_barrier sequence keeps the compiler from
-// moving the reads back next to their MFMAs (which exposes the LDS latency
-// once per batch) or hoisting them all (which costs registers). NSend DMA
-// slots (send(m)) are spread between the batches.
-template <int D, typename T, int NSend, class Send>
-__device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16 (&pf)[2],
+// Per-lane LDS byte addresses of the paired kernel's operand reads in stage
+// 0; stage s adds a compile-time offset, so with the stages unrolled every
+// read is base register + immediate and the MFMA phase spends no vector
+// instructions on addresses.
+//  - S operand (k[s], k-step s): row n (+ 32 for the second half), logical
+//    chunk 2 s + g, stored at chunk (2 s + g) ^ kswz(n).
+//  - V^T operand (v[d], dims tile d): rows r0 = 4 g + j / 4 (+ 8, + 16 u),
+//    bytes 32 half + 8 (j % 4) of 64-byte column group d, stored at group
+//    d ^ vswz(r0).
+template <int D> struct PairAddr {
+  static constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
+  uint32_t k[KS], v[DT];
+  __device__ __forceinline__ void init(uint32_t lds, int lane) {
+    using L = PairLds<D>;
+    const int n = lane & 31, g = lane >> 5, j = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+      k[st] = lds + 2 * L::kstage(0) + n * RB + 16 * ((2 * st + g) ^ L::kswz(n));
+    const int r0 = 4 * g + (j >> 2);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+      v[d] = lds + 2 * L::vstage(0) + r0 * RB + 32 * half + 8 * (j & 3) + 64 * (d ^ L::vswz(r0));
+  }
+};
+
+// The MFMA phase of a paired-group step: S = K Q^T for this tile (K stage
+// KST), then O^T += V^T P^T for the previous one (V stage VST). While the S
+// MFMAs run, the wave packs the previous tile's exponentials (pf, fp32) into
+// MFMA operands (pk) and adds their row sums to l, so that this vector work,
+// which has no MFMA dependency, fills the issue slots of the MFMA phase
+// instead of lengthening the VALU phase. Every LDS read is issued one batch
+// ahead of the MFMAs that consume it; the sched_group_barrier sequence keeps
+// the compiler from moving the reads back next to their MFMAs (which exposes
+// the LDS latency once per batch) or hoisting them all (which costs
+// registers).
+template <int D, typename T, int KST, int VST>
+__device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32x16 (&pf)[2],
                                                 float& l, f32x16 (&acc)[D / 32],
-                                                const uint16_t* Ks, const u32x4 (&qr)[D / 16],
-                                                f32x16 (&sc)[2], int lane, const Send& send) {
-  constexpr int KS = D / 16, DT = D / 32;
+                                                const u32x4 (&qr)[D / 16], f32x16 (&sc)[2]) {
+  using L = PairLds<D>;
+  constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
   constexpr int NQ = 2 * KS;      // S MFMAs: (half i % 2, k-step i / 2): two interleaved chains
   constexpr int NP = 4 * DT;      // PV MFMAs: (key step u = i / DT, dims tile d = i % DT)
   constexpr int NA = NQ + NP;
@@ -1173,24 +1204,17 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16
   constexpr int NQB = NQ / B, NPB = NP / B;
   static_assert(NQ % B == 0 && NP % B == 0, "batches must not mix PV and S MFMAs");
   static_assert(16 % NQB == 0, "the packing must split evenly over the S batches");
-  using L = PairLds<D>;
-  constexpr int RB = 2 * D;       // bytes per row
-  const int n = lane & 31, g = lane >> 5;
-  const int j = lane & 15, half = (lane >> 4) & 1;
-  // V^T operand: rows r0 (+ 8, + 16 u), bytes 32 half + 8 (j % 4) of 64-byte
-  // column group d, which sits at group d ^ vswz(r0).
-  const int r0 = 4 * g + (j >> 2);
-  const uint32_t vaddr = lds_addr(Vs) + r0 * RB + 32 * half + 8 * (j & 3) + 64 * L::vswz(r0);
-  // S operand: row n (+ 32), logical chunk 2 s + g at chunk (2 s + g) ^ kswz(n).
-  const uint32_t kaddr = lds_addr(Ks) + n * RB + 16 * (g ^ L::kswz(n));
+  constexpr uint32_t kOff = 2 * (L::kstage(KST) - L::kstage(0));
+  constexpr uint32_t vOff = 2 * (L::vstage(VST) - L::vstage(0));
+  static_assert(kOff + 64 * RB < 65536 && vOff + 64 * RB < 65536, "immediate offsets");
   auto vfrag = [&](int i) __attribute__((always_inline)) {
-    const uint32_t vu = (vaddr ^ (64 * (i % DT))) + 16 * (i / DT) * RB;
+    const uint32_t vu = ad.v[i % DT] + (vOff + 16 * (i / DT) * RB);
     const u32x2 lo = lds_read_tr16_at(vu);
     const u32x2 hi = lds_read_tr16_at(vu + 8 * RB);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
   auto kfrag = [&](int i) __attribute__((always_inline)) {
-    return lds_read_b128_at((kaddr ^ (32 * (i / 2))) + (i % 2) * 32 * RB);
+    return lds_read_b128_at(ad.k[i / 2] + (kOff + (i % 2) * 32 * RB));
   };
   // One sequence of A operands: S MFMAs first, then PV MFMAs.
   auto afrag = [&](int i) __attribute__((always_inline)) {
@@ -1231,14 +1255,10 @@ __device__ __forceinline__ void pair_mfma_phase(const uint16_t* Vs, const f32x16
         part[e & 1] = Mfma<T>::sum2(pp, part[e & 1]);
       }
     }
-#pragma unroll
-    for (int m = 0; m < NSend; ++m)
-      if (b == 1 + m * (NA / B) / (NSend > 0 ? NSend : 1)) send(m);
   }
   l += part[0] + part[1];
   // Schedule: batch b's MFMAs after the reads of batch b + 1 (two LDS reads
-  // per PV MFMA, one per S MFMA); the packing's vector instructions (two per
-  // pair) after each S batch's MFMAs.
+  // per PV MFMA, one per S MFMA).
   __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
 #pragma unroll
   for (int b = 0; b < NQB; ++b) {
@@ -1304,19 +1324,13 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 #pragma unroll
     for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
   }
-  // Three stages; step j (tile t_begin + j) uses stage j % 3 (j >= -1).
-  auto kbuf = [&](int j) __attribute__((always_inline)) {
-    return smem + ((j + 3) % 3) * PairLds<D>::stage;
-  };
-  auto vbuf = [&](int j) __attribute__((always_inline)) {
-    return smem + ((j + 3) % 3) * PairLds<D>::stage + PairLds<D>::kElems;
-  };
   using Dma = PairDma<D, T>;
   const uint32_t smem_b = lds_addr(smem);
   Dma dma;
   dma.init(wid, lane, src);
+  // K_0 into stage 0; V of step -1 (nothing: zeros) into V stage 2.
 #pragma unroll
-  for (int m = 0; m < Dma::NP; ++m) dma.issue(m, src, smem_b, t_begin, nt, 0, -1, wid);
+  for (int m = 0; m < Dma::NP; ++m) dma.issue(m, src, smem_b, t_begin, nt, 0, -1, 0, 2, wid);
   {
     const uint32_t qmask = qvalid ? ~0u : 0u;
     const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
@@ -1324,6 +1338,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
     for (int s = 0; s < KS; ++s) qr[s] = (qr[s] & qmask) ^ flip;
   }
   const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
+  PairAddr<D> ad;
+  ad.init(smem_b, lane);
 
   f32x16 acc[DT];
 #pragma unroll
@@ -1333,51 +1349,52 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   f32x16 sc[2];
   f32x16 pf[2];  // exponentials of the last tile, packed in the next MFMA phase
 
-  // The first MFMA phase runs its PV on V stage -1 with P = 0. Step -1's V
-  // slots above filled that stage with zeros, so whatever an earlier kernel
+  // The first MFMA phase runs its PV on V stage 2 (step -1) with P = 0. The
+  // V slots above filled that stage with zeros, so whatever an earlier kernel
   // left in LDS (NaN included) contributes exactly 0.
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of K_0 and of V stage -1
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of K_0 and of V stage 2
   __syncthreads();
 
   // The phase program, global phases p = -1 .. 2 nt (2 nt + 2 barriers for
-  // every wave). Group 0 runs MFMA phase j (PV_{j-1} and S_j) at p = 2j - 1
-  // and the VALU phase of tile j at p = 2j; group 1 runs each one phase
-  // later. Each group runs its own straight-line loop body, so its values
-  // keep their registers from one phase to the next.
+  // every wave). Group 0 runs MFMA phase j (S_j, PV_{j-1}) at p = 2j - 1 and
+  // the VALU phase of tile j at p = 2j; group 1 runs each one phase later.
+  // Each group runs its own straight-line loop body, so its values keep
+  // their registers from one phase to the next; the body is unrolled over
+  // the three stages (step j uses stage j mod 3), so that every LDS offset is
+  // an immediate.
   //
-  // DMA: during VALU phase j every wave sends its slots of step j
-  // (K_{j+2}, V_{j+1}), spread between the exponentials. K_{j+2}'s stage last held K_{j-1}, read in MFMA
-  // phases j-1 (p <= 2j - 2); V_{j+1}'s held V_{j-2}, read in the same
-  // phases: both free by p = 2j, group 0's send of step j. Step j's pieces
-  // are first read at p = 2j + 3; every wave has them waited for by the
-  // barrier ending p = 2j + 2. Group 0 sent step j + 1 at p = 2j + 2 and
-  // keeps those NP pieces in flight; group 1 (sends at odd p) has nothing
-  // newer and waits for all.
-  auto send = [&](int j) __attribute__((always_inline)) {
-    return [&, j](int m) __attribute__((always_inline)) {
-      dma.issue(m, src, smem_b, t_begin, nt, j + 2, j + 1, wid);
-    };
+  // DMA: during VALU phase j every wave sends its slots of step j (K_{j+2},
+  // V_{j+1}), spread between the exponentials. K_{j+2}'s stage last held
+  // K_{j-1}, read in MFMA phases j-1 (p <= 2j - 2); V_{j+1}'s held V_{j-2},
+  // read in the same phases: both free by p = 2j, group 0's send of step j.
+  // Step j's pieces are first read at p = 2j + 3; every wave has them waited
+  // for by the barrier ending p = 2j + 2. Group 0 sent step j + 1 at
+  // p = 2j + 2 and keeps those NP pieces in flight; group 1 (sends at odd p)
+  // has nothing newer and waits for all.
+  auto send = [&](int j, auto rc, int m) __attribute__((always_inline)) {
+    constexpr int R = decltype(rc)::value;  // j mod 3
+    dma.issue(m, src, smem_b, t_begin, nt, j + 2, j + 1, (R + 2) % 3, (R + 1) % 3, wid);
   };
   // One straight-line body for every MFMA phase: the first (j = 0) runs PV
   // with P = 0 (acc unchanged), the last (j = nt) computes an S that is never
   // used, from a stale but in-bounds K buffer. One extra tile of MFMAs per
-  // work item, against a single register allocation for the phase.
+  // work item, against a single register allocation for the phase. The wave
+  // in its MFMA phase issues ahead of its SIMD partner (raised priority): an
+  // MFMA it cannot issue idles the matrix pipe, while the partner's vector
+  // work fills whatever issue cycles are left.
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) pf[kt] = f32x16{};
-  // The wave in its MFMA phase issues ahead of its SIMD partner (raised
-  // priority): an MFMA it cannot issue idles the matrix pipe, while the
-  // partner's vector work fills whatever issue cycles are left.
-  auto mfma_phase = [&](int j) __attribute__((always_inline)) {
+  auto mfma_phase = [&](auto rc) __attribute__((always_inline)) {
+    constexpr int R = decltype(rc)::value;  // j mod 3: K stage R, V stage R - 1
     __builtin_amdgcn_s_setprio(1);
-    if (wave_active)
-      pair_mfma_phase<D, T, 0>(vbuf(j - 1), pf, sm.l, acc, kbuf(j), qr, sc, lane, send(j));
+    if (wave_active) pair_mfma_phase<D, T, R, (R + 2) % 3>(ad, pf, sm.l, acc, qr, sc);
     __builtin_amdgcn_s_setprio(0);
   };
   static_assert(Dma::NP == 4 || Dma::NP == 2, "DMA slots are spread over the 32 exponentials");
-  auto valu_phase = [&](int j) __attribute__((always_inline)) {
+  auto valu_phase = [&](int j, auto rc) __attribute__((always_inline)) {
     if (!wave_active) {
 #pragma unroll
-      for (int m = 0; m < Dma::NP; ++m) send(j)(m);
+      for (int m = 0; m < Dma::NP; ++m) send(j, rc, m);
     } else {
       const int t = t_begin + j;
       const bool in_cache = t < n_ct;
@@ -1391,7 +1408,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
         for (int r = 0; r < 16; ++r) {
           pf[kt][r] = fast_exp2(__builtin_fmaf(sc[kt][r], c, -mb));
           constexpr int every = 32 / Dma::NP;
-          if ((16 * kt + r) % every == every - 1) send(j)((16 * kt + r) / every);
+          if ((16 * kt + r) % every == every - 1) send(j, rc, (16 * kt + r) / every);
         }
     }
   };
@@ -1410,30 +1427,44 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  // Steps of one group: VALU phase j, then MFMA phase j + 1.
+  auto steps = [&](bool first_even) __attribute__((always_inline)) {
+    for (int j = 0;;) {
+      if (j >= nt) break;
+      valu_phase(j, S0{});
+      end_phase(first_even);
+      mfma_phase(S1{});
+      end_phase(!first_even);
+      if (++j >= nt) break;
+      valu_phase(j, S1{});
+      end_phase(first_even);
+      mfma_phase(S2{});
+      end_phase(!first_even);
+      if (++j >= nt) break;
+      valu_phase(j, S2{});
+      end_phase(first_even);
+      mfma_phase(S0{});
+      end_phase(!first_even);
+      ++j;
+    }
+  };
   if (grp == 0) {
 #pragma unroll
-    for (int m = 0; m < Dma::NP; ++m) send(-1)(m);
-    mfma_phase(0);           // p = -1
+    for (int m = 0; m < Dma::NP; ++m) send(-1, S2{}, m);
+    mfma_phase(S0{});        // p = -1
     end_phase(false);
-    for (int j = 0; j < nt; ++j) {
-      valu_phase(j);         // p = 2j
-      end_phase(true);
-      mfma_phase(j + 1);     // p = 2j + 1
-      end_phase(false);
-    }
+    steps(true);             // p = 2j (VALU), 2j + 1 (MFMA)
     end_phase(true);         // p = 2 nt
   } else {
 #pragma unroll
-    for (int m = 0; m < Dma::NP; ++m) send(-1)(m);
+    for (int m = 0; m < Dma::NP; ++m) send(-1, S2{}, m);
     end_phase(false);        // p = -1
-    mfma_phase(0);           // p = 0
+    mfma_phase(S0{});        // p = 0
     end_phase(true);
-    for (int j = 0; j < nt; ++j) {
-      valu_phase(j);         // p = 2j + 1
-      end_phase(false);
-      mfma_phase(j + 1);     // p = 2j + 2
-      end_phase(true);
-    }
+    steps(false);            // p = 2j + 1 (VALU), 2j + 2 (MFMA)
   }
   // The last sends (steps past the end, zeros) must land before the
   // workgroup's LDS is handed to the next one.
