@@ -99,6 +99,19 @@ struct AttnArgs {
   int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
 };
 
+// Touch every 64-byte line of the argument header up front: four
+// independent scalar loads and one wait, instead of the chain of dependent
+// loads (each a cache miss at kernel start) that the first uses would
+// otherwise issue one after another.
+__device__ __forceinline__ void prefetch_args(const AttnArgs& a) {
+  static_assert(offsetof(AttnArgs, n_seg) < 256, "argument header spans four lines");
+  const uint64_t l0 = reinterpret_cast<uint64_t>(a.q);
+  const uint64_t l1 = uint64_t(a.v_sb);
+  const uint64_t l2 = uint64_t(a.c_sh);
+  const uint32_t l3 = uint32_t(a.n_seg);
+  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3));
+}
+
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16_t> {
   static __device__ __forceinline__ f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
@@ -143,17 +156,27 @@ __device__ __forceinline__ int load_start(const AttnArgs& a, int i) {
 }
 
 // End (exclusive, in current-key coordinates) of the keys query i may see.
+// Block b spans [start_b, start_{b+1}) (the last one up to Lq), and a query
+// sees the keys up to the end of its own block. With the starts sorted that
+// end is the first start above i (Lq if none); a query before the first
+// start sees no new key. The starts are read 16 at a time, indices clamped
+// to the last one, so each batch is one round of independent scalar loads
+// instead of a chain of dependent ones.
 __device__ __forceinline__ int visible_end(const AttnArgs& a, int i) {
   if (a.causal) return i + 1;
   if (a.n_blocks == 0) return a.Lk;
-  int e = 0;
-  int s = load_start(a, 0);
-  for (int bi = 0; bi < a.n_blocks; ++bi) {
-    const int nx = (bi + 1 < a.n_blocks) ? load_start(a, bi + 1) : a.Lq;
-    if (s <= i && i < nx) e = max(e, nx);
-    s = nx;
+  const int nb = a.n_blocks;
+  int e = a.Lq, first = 0;
+  for (int base = 0; base < nb; base += 16) {
+    int st[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) st[u] = load_start(a, min(base + u, nb - 1));
+    if (base == 0) first = st[0];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (st[u] > i) e = min(e, st[u]);
   }
-  return min(e, a.Lq);
+  return i < first ? 0 : e;
 }
 
 // LDS geometry, per stage: a K tile [64 keys][D] and a V tile [64 keys][D],
@@ -392,8 +415,8 @@ struct TileDma {
   }
 };
 
-// LDS of the paired-group kernel: three stages (K tile + V tile each, rows
-// of D elements, no padding). Bank conflicts are avoided by
+// LDS of the paired-group kernel: NST stages (K tile + V tile each, rows
+// of D elements, no padding; three in the prefill kernel). Bank conflicts are avoided by
 // permuting the 16-byte chunks within each row instead of padding, so that
 // the DMA pieces are whole rows and the eight waves get the same number of
 // them:
@@ -409,11 +432,11 @@ struct TileDma {
 //    or row mod 4 (D = 64), group) pairs.
 // Both swizzles are invariant under the row offsets the reads add as
 // immediates (32 K rows, 8 and 16 V rows).
-template <int D> struct PairLds {
+template <int D, int NST = 3> struct PairLds {
   static constexpr int kElems = kBN * D, vElems = kBN * D;  // one tile each
-  static constexpr int stages = 3;
-  // Element offsets of stage s's K and V tiles: the three K tiles, then the
-  // three V tiles, so that every read offset fits the LDS instructions'
+  static constexpr int stages = NST;
+  // Element offsets of stage s's K and V tiles: the NST K tiles, then the
+  // NST V tiles, so that every read offset fits the LDS instructions'
   // 16-bit immediate (given a per-lane base that includes the V region's).
   static constexpr int kstage(int s) { return s * kElems; }
   static constexpr int vstage(int s) { return stages * kElems + s * vElems; }
@@ -434,8 +457,9 @@ template <int D> struct PairLds {
 // the work item still issue (and write zeros). The count of a wave's pieces in flight is therefore a
 // compile-time constant, which lets a wave wait for one step's pieces while
 // the next step's are still flying.
-template <int D, typename T>
+template <int D, typename T, int NST = 3>
 struct PairDma {
+  using L = PairLds<D, NST>;
   static constexpr int CR = D / 8;             // 16-byte chunks per row
   static constexpr int RPP = 64 / CR;          // rows per piece
   static constexpr int PK = kBN / RPP;         // pieces per K (or V) tile
@@ -450,7 +474,7 @@ struct PairDma {
 #pragma unroll
     for (int m = 0; m < NP; ++m) {
       const int r = (wid + kPairWaves * (m % NK)) * RPP + lane / CR, x = lane % CR;
-      const int c = m < NK ? x ^ PairLds<D>::kswz(r) : x ^ (4 * PairLds<D>::vswz(r));
+      const int c = m < NK ? x ^ L::kswz(r) : x ^ (4 * L::vswz(r));
       const uint32_t sn = uint32_t(m < NK ? src.k_sl2 : src.v_sl2);
       on[m] = uint32_t(r) * sn + uint32_t(c * 16);
       dc[m] = uint32_t(r) * (uint32_t(src.c_ss2) - sn);
@@ -482,7 +506,7 @@ struct PairDma {
     const uint32_t base = live ? uint32_t(row0) * uint32_t(stride) : 0x80000000u;
     const uint32_t cmask = in_cache ? ~0u : 0u;
     const int p = wid + kPairWaves * (m % NK);
-    const int at = (is_k ? PairLds<D>::kstage(kst) : PairLds<D>::vstage(vst)) + p * 512;
+    const int at = (is_k ? L::kstage(kst) : L::vstage(vst)) + p * 512;
     dma_piece_at(r, lds + 2 * at, on[m] + (dc[m] & cmask) + base);
   }
 };
@@ -875,6 +899,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
   constexpr int DT = D / 32;  // 32-wide head_dim tiles of the output
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  prefetch_args(a);
 
   const Coord it = locate(a, blockIdx.x, false, 0);
   const int b = it.b, h = it.h;
@@ -1165,11 +1190,11 @@ __device__ __forceinline__ void pv_packed(const uint16_t* Vs, const u32x4 (&pk)[
 //  - V^T operand (v[d], dims tile d): rows r0 = 4 g + j / 4 (+ 8, + 16 u),
 //    bytes 32 half + 8 (j % 4) of 64-byte column group d, stored at group
 //    d ^ vswz(r0).
-template <int D> struct PairAddr {
+template <int D, int NST = 3> struct PairAddr {
   static constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
   uint32_t k[KS], v[DT];
   __device__ __forceinline__ void init(uint32_t lds, int lane) {
-    using L = PairLds<D>;
+    using L = PairLds<D, NST>;
     const int n = lane & 31, g = lane >> 5, j = lane & 15, half = (lane >> 4) & 1;
 #pragma unroll
     for (int st = 0; st < KS; ++st)
@@ -1206,7 +1231,7 @@ __device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32
   static_assert(16 % NQB == 0, "the packing must split evenly over the S batches");
   constexpr uint32_t kOff = 2 * (L::kstage(KST) - L::kstage(0));
   constexpr uint32_t vOff = 2 * (L::vstage(VST) - L::vstage(0));
-  static_assert(kOff + 64 * RB < 65536 && vOff + 64 * RB < 65536, "immediate offsets");
+  static_assert(kOff + 32 * RB < 65536 && vOff + 56 * RB < 65536, "immediate offsets");
   auto vfrag = [&](int i) __attribute__((always_inline)) {
     const uint32_t vu = ad.v[i % DT] + (vOff + 16 * (i / DT) * RB);
     const u32x2 lo = lds_read_tr16_at(vu);
@@ -1278,6 +1303,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int BM = kBMPair;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  prefetch_args(a);
 
   const Coord it = locate(a, blockIdx.x, false, 0);
   const int b = it.b, h = it.h;
@@ -1487,6 +1513,7 @@ template <int D> struct CombineShape {
 // (batch, head) run on the XCD whose L2 holds that head's partials.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  prefetch_args(a);
   using CS = CombineShape<D>;
   const Coord cd = locate(a, blockIdx.x, true, a.bm / CS::RPB);
   const int row = cd.split * CS::RPB + threadIdx.x / CS::TPR;
