@@ -921,10 +921,16 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 
   // Key range of the workgroup. Block starts are sorted ascending, so the
   // visible end is non-decreasing in the query index: the first and last
-  // queries bound it. Workgroup-uniform (scalar) work, no barrier, so the
-  // tile loads below go out right away.
-  const int kv_min = cache_len + visible_end(a, q0);
-  const int kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
+  // queries bound it. Workgroup-uniform (scalar) work, no barrier. The
+  // dual-stream (decode) path tiles the largest range any query of the chunk
+  // can see (the whole cache and all Lq new keys) so that its tile loads go
+  // out before the block starts are read; it skips the tiles past the
+  // visible range and masks the straddling ones per key.
+  int kv_min = 0, kv_max = cache_len + a.Lq;
+  if (NS == 1) {
+    kv_min = cache_len + visible_end(a, q0);
+    kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
+  }
 
   const int n_ct = (cache_len + kBN - 1) / kBN;
   const int n_tiles = n_ct + (kv_max - cache_len + kBN - 1) / kBN;
@@ -957,16 +963,19 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   // is a (wave-uniform) branch around fixed-index loops.
   constexpr int KQ = KS / NS;  // k-steps this stream fetches
   u32x4 qr[KS];
-  // Rows past the end load the last row (an address in bounds, no branch)
-  // and are zeroed once the tile loads are out.
-  const uint16_t* qp =
-      a.q + b * a.q_sb + int64_t(min(qi, a.Lq - 1)) * a.q_sl + h * a.q_sh + 8 * g;
-  if (stream == 0) {
 #pragma unroll
-    for (int s = 0; s < KQ; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
-  } else {
+  for (int s = 0; s < KS; ++s) qr[s] = u32x4{0, 0, 0, 0};
+  // Rows past the end load nothing (a CU takes in 64 bytes per clock, and a
+  // short chunk leaves many rows of the last query tile empty).
+  const uint16_t* qp = a.q + b * a.q_sb + int64_t(qvalid ? qi : 0) * a.q_sl + h * a.q_sh + 8 * g;
+  if (qvalid) {
+    if (stream == 0) {
 #pragma unroll
-    for (int s = KQ; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+      for (int s = 0; s < KQ; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+    } else {
+#pragma unroll
+      for (int s = KQ; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+    }
   }
 
   TileRegs<D> regs;
@@ -980,7 +989,11 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       dma.issueV(src, t_begin, wave, smem + Lds<D>::kElems);
     }
   } else {
+    // The stream's first tile into registers right away. (Fetching the
+    // second one too delays the first: a CU takes in 64 bytes per clock.)
     regs.load(ltid, src, t_first, t_first < t_end);
+    kv_min = cache_len + visible_end(a, q0);
+    kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
   }
 
   // Visible-key end of this lane's query (per-key masking of straddling tiles).
@@ -1061,7 +1074,8 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   } else {
   // Each stream double-buffers its tiles in its own LDS region. A buffer is
   // rewritten two rounds after it was read, past the barrier of the round in
-  // between, which every wave has reached.
+  // between, which every wave has reached. Tiles past the workgroup's
+  // visible keys are skipped.
   uint16_t* const region = smem + stream * 2 * Lds<D>::stage;
   for (int i = 0; i < iters; ++i) {
     const int t = t_first + i * NS;
@@ -1069,7 +1083,9 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     if (t < t_end) regs.store(ltid, st, st + Lds<D>::kElems);
     __syncthreads();
     if (t + NS < t_end) regs.load(ltid, src, t + NS, true);
-    if (wave_active && t < t_end) {
+    const bool in_cache = t < n_ct;
+    const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
+    if (wave_active && t < t_end && j0 < kv_max) {
       int lim;
       bool masked;
       tile_mask(t, lim, masked);
