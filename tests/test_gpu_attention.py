@@ -294,3 +294,51 @@ def test_default_scale(device, built_lib):
     a = ops.blockwise_causal_attention(q, k, v)
     b = ops.blockwise_causal_attention(q, k, v, softmax_scale=1.0 / math.sqrt(64))
     assert torch.equal(a, b)
+
+
+# Prefill-shaped calls run on the paired-group kernel (two four-wave groups
+# half a tile apart, three LDS stages, its loops unrolled over the stages);
+# DX_ATTN_STREAMS=1 forces the plain single-stream schedule, whose arithmetic
+# is the same in the same order (with one split, so no partials are rounded;
+# tiles a 256-row item visits past a 128-row item's range are fully masked
+# for the earlier rows and add exact zeros). Tile counts 1..7 per work item cover every
+# stage residue and loop exit; the cache cases put a partial tile at the
+# cache boundary, and 300 rows leave the second work item's group 1 partly
+# and wholly idle.
+@pytest.mark.parametrize("d,dtype,q_len,cache_len,blocks", [
+    (128, torch.bfloat16, 64, 0, None),
+    (128, torch.bfloat16, 128, 0, None),
+    (128, torch.bfloat16, 192, 0, None),
+    (128, torch.bfloat16, 256, 0, None),
+    (128, torch.bfloat16, 320, 0, None),
+    (128, torch.bfloat16, 384, 0, None),
+    (128, torch.bfloat16, 448, 0, None),
+    (128, torch.bfloat16, 300, 100, [0, 96, 160]),
+    (128, torch.float16, 256, 200, [0, 128]),
+    (64, torch.bfloat16, 300, 0, [0, 96, 160]),
+    (64, torch.float16, 192, 100, None),
+])
+def test_prefill_schedules_agree_bit_exact(device, built_lib, monkeypatch, d, dtype, q_len,
+                                           cache_len, blocks):
+    h = 4
+    q = _rand((1, q_len, h, d), device, dtype=dtype, scale=0.5, seed=71)
+    k = _rand((1, q_len, h, d), device, dtype=dtype, seed=72)
+    v = _rand((1, q_len, h, d), device, dtype=dtype, seed=73)
+    cache = (_rand((2, 1, cache_len + q_len, h, d), device, dtype=dtype, scale=0.5, seed=74)
+             if cache_len else None)
+    bb = torch.tensor(blocks, device=device) if blocks else None
+
+    monkeypatch.setenv("DX_ATTN_SPLITS", "1")  # whole key ranges: no partials to round
+
+    def run(streams):
+        monkeypatch.setenv("DX_ATTN_STREAMS", str(streams))
+        return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
+                                              block_boundaries=bb)
+
+    paired, single = run(3), run(1)
+    torch.cuda.synchronize()
+    assert torch.equal(paired, single) or (
+        torch.isnan(paired).equal(torch.isnan(single))
+        and torch.equal(paired.nan_to_num(), single.nan_to_num()))
+    assert_parity(paired, _oracle(q, k, v, cache, cache_len, bb),
+                  what=f"d={d} {dtype} q_len={q_len} cache_len={cache_len} blocks={blocks}")
