@@ -1642,15 +1642,19 @@ int choose_uniform_splits(int64_t units, int64_t Lq, int64_t tiles, int cus, int
                                                       cdiv(tiles, 2)}));
   } else {
     // Paired groups: 256 queries per workgroup, one workgroup per CU; the
-    // split minimising rounds x tiles-per-split, with a small cost per extra
-    // split (partials + merge).
+    // split minimising rounds x (tiles per split + a fixed cost per work
+    // item, about 8 tiles: its start-up, its stores, and the K/V its key
+    // range pulls that another query tile of the head already read), plus
+    // 2 tiles per split for partials and merge. Calibrated at the Wan-14B
+    // chunk (160 groups of 130 tiles): measured 1..10 splits order as this
+    // cost does, 3 best (179 us, against 208 us at 8 and 188 us at 1).
     streams = 3;
     const int64_t groups = units * cdiv(Lq, kBMPair);
     if (groups < 2 * cus && tiles >= 8) {
       double best = 1e30;
       for (int64_t s = 1; s <= kMaxSplits && s <= tiles / 4; ++s) {
-        const double cost = double(cdiv(groups * s, cus)) * double(cdiv(tiles, s)) +
-                            (s > 1 ? 0.5 * double(s) + 1.0 : 0.0);
+        const double cost = double(cdiv(groups * s, cus)) * double(cdiv(tiles, s) + 8) +
+                            (s > 1 ? 2.0 * double(s) : 0.0);
         if (cost < best - 1e-9) { best = cost; best_s = s; }
       }
     }
