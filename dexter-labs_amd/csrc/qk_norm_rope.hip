@@ -92,8 +92,21 @@ struct RopeArgs {
   float eps;
 };
 
+// Touch every 64-byte line of the arguments up front: independent scalar
+// loads and one wait, instead of the chain of dependent loads (each a cache
+// miss at kernel start) that the first uses would otherwise issue.
+__device__ __forceinline__ void prefetch_args(const RopeArgs& a) {
+  static_assert(sizeof(RopeArgs) <= 256, "arguments span at most four lines");
+  const uint64_t l0 = reinterpret_cast<uint64_t>(a.q);
+  const uint64_t l1 = uint64_t(a.v_sb);
+  const uint64_t l2 = reinterpret_cast<uint64_t>(a.q_out);
+  const uint32_t l3 = uint32_t(a.L);
+  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3));
+}
+
 template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND>
 __global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
+  prefetch_args(a);
   __shared__ float red[2][kMaxThreads / 64];
   const int token = blockIdx.x;  // b * L + l
   const int b = token / a.L, l = token % a.L;
