@@ -224,6 +224,54 @@ def run_config(name: str, device, reps: int) -> dict:
     }
 
 
+def run_norm(device, layers: int, reps: int) -> dict:
+    """adaLN modulation and gated residual (the ops either side of attention in a Wan
+    block) at the C1 activation (83 x 3072) and the C2 prefill activation
+    (8,192 x 3072), bf16, [1, 1, C] modulation rows as the model passes them.
+    Each figure is one launch, event-timed inside a graph of distinct inputs, next to
+    the reference's unfused torch expression (``ops/reference/norm.py:20,25``) timed
+    the same way."""
+    import torch
+    import torch.nn.functional as F
+
+    import dexter_amd.ops as ops
+    from dexter_amd.bench import harness
+
+    out = {}
+    g = torch.Generator(device=device).manual_seed(0)
+    for name, rows, n in (("C1", 83, layers), ("C2", 8192, 4)):
+        cols = 3072
+        xs = [torch.randn(1, rows, cols, device=device, generator=g).to(torch.bfloat16)
+              for _ in range(n)]
+        ys = [torch.randn_like(x) for x in xs]
+        mod = torch.randn(n, 6, 1, cols, device=device, generator=g).to(torch.bfloat16)
+        parts = [m.unsqueeze(0).unbind(1) for m in mod]  # [1, 1, C] views, as the model's
+        act = rows * cols * 2
+        row = cols * 2
+        cases = {
+            "adaln": (lambda i: ops.adaln_modulate(xs[i], parts[i][1], parts[i][0], 1e-6),
+                      lambda i: F.layer_norm(xs[i], (cols,), eps=1e-6) * (1 + parts[i][1])
+                      + parts[i][0],
+                      2 * act + 2 * row),
+            "gated_residual": (lambda i: ops.gated_residual(xs[i], ys[i], parts[i][2]),
+                               lambda i: xs[i] + ys[i] * parts[i][2],
+                               3 * act + row),
+        }
+        for op, (fused, ref, nbytes) in cases.items():
+            fg = harness.capture(lambda f=fused: [f(i) for i in range(n)])
+            ms = harness.event_time_ms(fg.replay, reps=reps) / n
+            rg = harness.capture(lambda f=ref: [f(i) for i in range(n)])
+            rms = harness.event_time_ms(rg.replay, reps=reps) / n
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            out[f"{op}_{name}"] = {
+                "us": ms * 1e3, "gbps": gbps, "pct_hbm_peak": 100 * gbps / PEAK_HBM_GBPS,
+                "bytes": nbytes, "torch_unfused_us": rms * 1e3, "speedup_vs_torch": rms / ms,
+                "shape": [1, rows, cols]}
+            del fg, rg
+        del xs, ys, mod, parts
+    return out
+
+
 def run_cpu_baseline(inp, budget_s: float) -> dict:
     """The torch fp32 oracle on this host's cores, C1 attention per layer (a bounded sample)."""
     import platform as pyplatform
@@ -270,7 +318,7 @@ def main() -> int:
                     help="seconds of CPU work for the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip C2/C3/C4")
-    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4"], default=None,
+    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm"], default=None,
                     help="time one config's attention only (for profiling runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run a plain device copy of this size (counter calibration)")
@@ -303,6 +351,10 @@ def main() -> int:
         print(f"copy calibration: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
         del src, dst
 
+    if args.only == "norm":
+        res = run_norm(device, args.layers, reps=max(10, args.steps))
+        print(json.dumps({"only": args.only, **res}), flush=True)
+        return 0
     if args.only:
         res = run_config(args.only, device, reps=max(10, args.steps))
         print(json.dumps({"only": args.only, **res}), flush=True)
@@ -316,6 +368,9 @@ def main() -> int:
         for name, reps in (("C2", 20), ("C3", 20), ("C4", 50)):
             extra[name] = run_config(name, device, reps)
             print(f"{name} done: {extra[name]['us']:.1f} us", file=sys.stderr, flush=True)
+        extra["norm"] = run_norm(device, args.layers, reps=20)
+        print("norm done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["norm"].items()),
+              file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else run_cpu_baseline(head["inputs"], args.cpu_budget)
 
     line = {

@@ -10,6 +10,10 @@ and calls it, exactly as dexter's dispatchers do (``python/dexter/ops/__init__.p
 * ``kv_cache_append``            -> ``select("cache", "append", cache, k, v)``
   (no dispatcher in the reference: ``KVCache.append`` does two torch slice
   copies, ``models/dreamzero/model.py:53-58``; here it is a kernel too)
+* ``adaln_modulate``             -> ``select("norm", "adaln", x, scale, shift)``
+  (reference ``ops/__init__.py:39-49``; same arguments and default eps)
+* ``gated_residual``             -> ``select("norm", "gated_residual", x, y, gate)``
+  (reference ``ops/__init__.py:52-54``)
 
 Importing this module registers the gfx950 HIP kernels. Nothing else is
 registered, so on a machine without an MI355X every call raises
@@ -23,7 +27,27 @@ import torch
 from ..registry import select
 
 __all__ = ["qk_norm_rope", "blockwise_causal_attention", "kv_cache_append",
-           "qk_norm_rope_append", "blockwise_causal_attention_varlen"]
+           "qk_norm_rope_append", "blockwise_causal_attention_varlen",
+           "adaln_modulate", "gated_residual"]
+
+
+def adaln_modulate(
+    x: torch.Tensor,
+    scale: torch.Tensor,
+    shift: torch.Tensor,
+    eps: float = 1e-6,
+) -> torch.Tensor:
+    """``layer_norm(x) * (1 + scale) + shift`` in one pass.
+
+    ``x`` is ``[B, L, C]``; ``scale``/``shift`` are ``[B, L, C]`` or ``[B, 1, C]``
+    (any shape that broadcasts to ``x``'s rows, ``[C]`` included).
+    """
+    return select("norm", "adaln", x, scale, shift)(x, scale, shift, eps)
+
+
+def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """``x + y * gate``, fused so the residual is read and written once."""
+    return select("norm", "gated_residual", x, y, gate)(x, y, gate)
 
 
 def qk_norm_rope(

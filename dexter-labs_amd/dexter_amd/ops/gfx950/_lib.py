@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -81,6 +81,18 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         _p, _l, _p]),
     "dx_attention_workspace_bytes": (_l, [_l, _l, _l, _l, _l, _l,
                                           ctypes.POINTER(ctypes.c_int64)]),
+    "dx_adaln_modulate": (_i, [
+        _p, _l, _l, _i,            # x, sb, sl, x dtype
+        _p, _l, _l,                # scale, sb, sl
+        _p, _l, _l, _i,            # shift, sb, sl, modulation dtype
+        _p, _l, _l, _i,            # out, sb, sl, out dtype
+        _l, _l, _l, _f, _p]),      # B, L, C, eps, stream
+    "dx_gated_residual": (_i, [
+        _p, _l, _l,                # x, sb, sl
+        _p, _l, _l, _i,            # y, sb, sl, x/y dtype
+        _p, _l, _l, _i,            # gate, sb, sl, gate dtype
+        _p, _l, _l, _i,            # out, sb, sl, out dtype
+        _l, _l, _l, _p]),          # B, L, C, stream
 }
 
 _lock = threading.Lock()

@@ -19,6 +19,12 @@
  *                            the same with one cache length per sequence; the
  *                            reference has a scalar cache_len only, and a
  *                            ragged batch there is one call per sequence.
+ *   dx_adaln_modulate        ops/gfx1151/norm/adaln.py:108-128 (kernel :20-48;
+ *                            semantics ops/reference/norm.py:16-20, dispatcher
+ *                            ops/__init__.py:39-49)
+ *   dx_gated_residual        ops/gfx1151/norm/adaln.py:131-148 (kernel :51-67;
+ *                            semantics ops/reference/norm.py:23-25, dispatcher
+ *                            ops/__init__.py:52-54)
  *
  * Conventions
  *  - Tensors are device pointers with explicit element strides; the last
@@ -59,7 +65,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 2
+#define DX_ABI_VERSION 3
 
 /*
  * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.
@@ -173,6 +179,40 @@ int dx_blockwise_causal_attention_varlen(
 int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
                                      int64_t D, int64_t cache_len,
                                      const int64_t* cache_lens);
+
+/*
+ * Adaptive LayerNorm modulation of a [B, L, C] activation:
+ *   out = layer_norm(x over C, no affine, eps) * (1 + scale) + shift
+ * (ops/reference/norm.py:16-20). Statistics and arithmetic in fp32 with one
+ * final rounding (the math of ops/gfx1151/norm/adaln.py:36-48). scale and
+ * shift are [B, L, C] through their strides: stride 0 broadcasts, so a
+ * [B, 1, C] modulation takes sc_sl = 0 and a [C] one takes sc_sb = sc_sl = 0.
+ * The last dim of every operand is contiguous. scale and shift share
+ * mod_dtype; out_dtype must be the torch promotion of x_dtype and mod_dtype
+ * (equal types stay, any other pair is DX_F32). Dtypes: DX_BF16, DX_F16, DX_F32.
+ * C <= 65536 for 16-bit x, 32768 for f32 x.
+ * Replaces: ops/gfx1151/norm/adaln.py:108-128.
+ */
+int dx_adaln_modulate(const void* x, int64_t x_sb, int64_t x_sl, int x_dtype,
+                      const void* scale, int64_t sc_sb, int64_t sc_sl,
+                      const void* shift, int64_t sh_sb, int64_t sh_sl, int mod_dtype,
+                      void* out, int64_t o_sb, int64_t o_sl, int out_dtype,
+                      int64_t B, int64_t L, int64_t C, float eps, void* stream);
+
+/*
+ * Gated residual of [B, L, C] activations: out = x + y * gate
+ * (ops/reference/norm.py:23-25), as an fp32 product and an fp32 sum, each
+ * rounded, then one rounding to out_dtype. x and y share x_dtype; gate is
+ * [B, L, C] through its strides (0 broadcasts) with gate_dtype; out_dtype
+ * must be the promotion of x_dtype and gate_dtype. Same limits as
+ * dx_adaln_modulate.
+ * Replaces: ops/gfx1151/norm/adaln.py:131-148.
+ */
+int dx_gated_residual(const void* x, int64_t x_sb, int64_t x_sl,
+                      const void* y, int64_t y_sb, int64_t y_sl, int x_dtype,
+                      const void* gate, int64_t g_sb, int64_t g_sl, int gate_dtype,
+                      void* out, int64_t o_sb, int64_t o_sl, int out_dtype,
+                      int64_t B, int64_t L, int64_t C, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,8 +14,13 @@ under ``python/dexter/`` of raikonenfnu/dexter-labs):
                  (``ops/reference/rope.py:10-56``), with its intermediate
                  rounding to the input dtype.
 * ``kv_cache``   the KV-cache append/commit contract (``models/dreamzero/model.py:35-65``).
-* ``brute``      fp64 brute force (numpy, explicit loops) of attention and the
-                 prologue, written independently of the torch restatements;
+* ``norm``       torch restatement of the reference adaLN modulation and gated
+                 residual (``ops/reference/norm.py:16-25``), with the reference's
+                 per-op rounding, plus the single-rounding forms the fused
+                 kernels compute.
+* ``brute``      fp64 brute force (numpy, explicit loops) of attention, the
+                 prologue and the adaLN/gated-residual pair, written
+                 independently of the torch restatements;
                  the tests pin the restatements against it, against
                  ``torch.nn.functional.scaled_dot_product_attention`` and
                  against closed forms.

@@ -92,3 +92,39 @@ def qk_norm_rope(x, weight, cos, sin, eps=1e-6, interleaved=True, round_to=None)
         out[..., :half] = lo * c - hi * s
         out[..., half:] = lo * s + hi * c
     return out
+
+
+def adaln_modulate(x, scale, shift, eps=1e-6, round_to=None):
+    """LayerNorm (no affine) of each row of ``x [..., C]`` then ``* (1 + scale) + shift``,
+    in fp64 with explicit per-row loops.
+
+    LayerNorm here is the textbook one: the row mean, the biased variance
+    (divide by C), and ``(x - mean) / sqrt(var + eps)``. ``scale``/``shift``
+    broadcast against ``x`` as numpy arrays do. ``round_to`` (a callable
+    float64 -> float64) models the reference's rounding after each op:
+    after the norm, after ``1 + scale``, after the product and after the sum.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    scale = np.asarray(scale, dtype=np.float64)
+    shift = np.asarray(shift, dtype=np.float64)
+    shape = np.broadcast_shapes(x.shape, scale.shape, shift.shape)
+    rows = x.reshape(-1, x.shape[-1])
+    normed = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        row = rows[r]
+        n = row.shape[0]
+        mean = sum(float(v) for v in row) / n
+        var = sum((float(v) - mean) ** 2 for v in row) / n
+        normed[r] = (row - mean) / math.sqrt(var + eps)
+    normed = normed.reshape(x.shape)
+    rnd = round_to if round_to is not None else (lambda a: a)
+    gain = rnd(1.0 + scale)
+    prod = rnd(np.broadcast_to(rnd(normed), shape) * gain)
+    return rnd(prod + shift)
+
+
+def gated_residual(x, y, gate, round_to=None):
+    """``x + y * gate`` in fp64; ``round_to`` rounds the product and the sum."""
+    x, y, gate = (np.asarray(t, dtype=np.float64) for t in (x, y, gate))
+    rnd = round_to if round_to is not None else (lambda a: a)
+    return rnd(x + rnd(y * gate))

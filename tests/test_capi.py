@@ -27,7 +27,8 @@ def test_header_declares_the_path():
     names = declared_functions()
     for want in ("dx_qk_norm_rope", "dx_qk_norm_rope_append", "dx_kv_append",
                  "dx_blockwise_causal_attention", "dx_blockwise_causal_attention_varlen",
-                 "dx_attention_workspace_bytes", "dx_last_error", "dx_abi_version"):
+                 "dx_attention_workspace_bytes", "dx_last_error", "dx_abi_version",
+                 "dx_adaln_modulate", "dx_gated_residual"):
         assert want in names
 
 
@@ -85,3 +86,27 @@ def test_bad_arguments_are_rejected(built_lib):
     assert rc == _lib.DX_EINVAL and "must equal q length" in lib.dx_last_error().decode()
     with pytest.raises(ValueError, match="must equal q length"):
         _lib.check(rc, "attention")
+
+
+def test_norm_entry_points_validate_before_any_launch(built_lib):
+    lib = _lib.load()
+    bf, f32 = _lib.DX_BF16, _lib.DX_F32
+    # Empty rows: success, nothing launched (null pointers are never touched).
+    assert lib.dx_adaln_modulate(None, 0, 0, bf, None, 0, 0, None, 0, 0, bf,
+                                 None, 0, 0, bf, 1, 0, 3072, 1e-6, None) == _lib.DX_OK
+    assert lib.dx_gated_residual(None, 0, 0, None, 0, 0, bf, None, 0, 0, bf,
+                                 None, 0, 0, bf, 0, 5, 3072, None) == _lib.DX_OK
+    rc = lib.dx_adaln_modulate(None, 0, 0, 7, None, 0, 0, None, 0, 0, bf,
+                               None, 0, 0, bf, 1, 1, 64, 1e-6, None)
+    assert rc == _lib.DX_EINVAL and "dtype codes" in lib.dx_last_error().decode()
+    rc = lib.dx_adaln_modulate(None, 0, 0, bf, None, 0, 0, None, 0, 0, f32,
+                               None, 0, 0, bf, 1, 1, 64, 1e-6, None)
+    assert rc == _lib.DX_EINVAL and "promotion" in lib.dx_last_error().decode()
+    rc = lib.dx_gated_residual(None, 0, 0, None, 0, 0, bf, None, 0, 0, bf,
+                               None, 0, 0, bf, 1, 1, 1 << 20, None)
+    assert rc == _lib.DX_EINVAL and "exceeds" in lib.dx_last_error().decode()
+    rc = lib.dx_gated_residual(None, 0, 0, None, 0, 0, bf, None, 0, 0, bf,
+                               None, 0, 0, bf, 70000, 1, 64, None)
+    assert rc == _lib.DX_EINVAL and "grid limits" in lib.dx_last_error().decode()
+    with pytest.raises(ValueError, match="grid limits"):
+        _lib.check(rc, "gated_residual")

@@ -9,7 +9,9 @@ rounding step) fails at least one:
 * a library routine: ``torch.nn.functional.scaled_dot_product_attention``;
 * closed forms: identical keys average exactly the visible values; one-hot
   values read out the attention probabilities; RoPE preserves pair norms;
-  ``cos=1, sin=0`` reduces to the plain RMS norm.
+  ``cos=1, sin=0`` reduces to the plain RMS norm; adaLN with zero modulation
+  is ``torch.nn.functional.layer_norm``, a hand-computed row gives known
+  values, and a constant shift of x changes nothing; a zero gate returns x.
 
 The last tests plant mistakes in copies of the oracle and check the pins
 catch them.
@@ -27,6 +29,7 @@ import torch.nn.functional as F
 from oracle import attention as oatt
 from oracle import brute
 from oracle import kv_cache as okv
+from oracle import norm as onorm
 from oracle import rope as orope
 
 
@@ -307,3 +310,123 @@ def test_scale_default_is_inverse_sqrt_head_dim():
     a = oatt.blockwise_causal_attention(q, k, v)
     b = oatt.blockwise_causal_attention(q, k, v, softmax_scale=1 / math.sqrt(16))
     assert torch.equal(a, b)
+
+
+# ---------------------------------------------------- adaLN / gated residual -----
+
+def _norm_inputs(seed=0, b=2, l=5, c=64, dtype=torch.bfloat16, mod_rows=1):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, l, c, generator=g).to(dtype)
+    scale = torch.randn(b, mod_rows, c, generator=g).to(dtype)
+    shift = torch.randn(b, mod_rows, c, generator=g).to(dtype)
+    return x, scale, shift
+
+
+def _adaln_known_case():
+    """x = [0, 1, 2, 3]: mean 1.5, biased variance 1.25; with eps 0.75 the
+    denominator is sqrt(2). Gains 1 + scale = [2, 1, 0, 1.5]."""
+    x = torch.tensor([[0.0, 1.0, 2.0, 3.0]], dtype=torch.float64)
+    scale = torch.tensor([1.0, 0.0, -1.0, 0.5], dtype=torch.float64)
+    shift = torch.tensor([0.0, 1.0, 2.0, 3.0], dtype=torch.float64)
+    r2 = math.sqrt(2.0)
+    expect = torch.tensor([[-1.5 / r2 * 2, -0.5 / r2 + 1, 2.0, 1.5 / r2 * 1.5 + 3]],
+                          dtype=torch.float64)
+    return x, scale, shift, 0.75, expect
+
+
+def test_adaln_known_answer():
+    x, scale, shift, eps, expect = _adaln_known_case()
+    got = onorm.adaln_modulate_exact(x, scale, shift, eps)
+    torch.testing.assert_close(got, expect, rtol=0, atol=1e-12)
+    got = onorm.adaln_modulate(x.float(), scale.float(), shift.float(), eps)
+    torch.testing.assert_close(got.double(), expect, rtol=0, atol=1e-6)
+    got = brute.adaln_modulate(x.numpy(), scale.numpy(), shift.numpy(), eps)
+    np.testing.assert_allclose(got, expect.numpy(), rtol=0, atol=1e-12)
+
+
+def test_adaln_zero_modulation_is_layer_norm():
+    x, _, _ = _norm_inputs(dtype=torch.float64)
+    zero = torch.zeros(x.shape[-1], dtype=torch.float64)
+    lib = F.layer_norm(x, (x.shape[-1],), eps=1e-6)
+    torch.testing.assert_close(onorm.adaln_modulate_exact(x, zero, zero), lib, rtol=0, atol=1e-12)
+    torch.testing.assert_close(torch.from_numpy(brute.adaln_modulate(x.numpy(), 0.0, 0.0)), lib,
+                               rtol=0, atol=1e-12)
+
+
+def test_adaln_exact_matches_fp64_brute_force():
+    x, scale, shift = _norm_inputs(c=96)
+    got = onorm.adaln_modulate_exact(x, scale, shift, 1e-6, out_dtype=torch.float64)
+    ref = brute.adaln_modulate(x.double().numpy(), scale.double().numpy(), shift.double().numpy())
+    np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=1e-12)
+
+
+def test_adaln_matches_fp64_with_the_reference_rounding():
+    x, scale, shift = _norm_inputs(c=128, l=8)
+    got = onorm.adaln_modulate(x, scale, shift).double().numpy()
+    ref = brute.adaln_modulate(x.double().numpy(), scale.double().numpy(), shift.double().numpy(),
+                               round_to=_bf16_round)
+    # torch normalises in fp32 before its bf16 rounding, the brute force in
+    # fp64: a rare element lands on the other side of a rounding tie.
+    assert np.mean(got == ref) > 0.99
+    assert np.abs(got - ref).max() <= 0.05 * np.abs(ref).max()
+
+
+def test_adaln_output_dtype_is_the_promotion():
+    x, scale, shift = _norm_inputs()
+    assert onorm.adaln_modulate(x, scale, shift).dtype == torch.bfloat16
+    assert onorm.adaln_modulate(x, scale.float(), shift.float()).dtype == torch.float32
+    assert onorm.adaln_modulate_exact(x, scale.half(), shift.half()).dtype == torch.float32
+
+
+def test_adaln_shift_of_x_changes_nothing():
+    x, scale, shift = _norm_inputs(dtype=torch.float64)
+    a = onorm.adaln_modulate_exact(x, scale, shift)
+    b = onorm.adaln_modulate_exact(x + 7.0, scale, shift)
+    torch.testing.assert_close(a, b, rtol=0, atol=1e-9)
+
+
+def test_gated_residual_closed_forms():
+    x, y, _ = _norm_inputs()
+    zero, one = torch.zeros(1, 1, x.shape[-1]), torch.ones(1, 1, x.shape[-1])
+    assert torch.equal(onorm.gated_residual_fp32(x, y, zero.bfloat16()), x)
+    assert torch.equal(onorm.gated_residual(x, y, zero.bfloat16()), x)
+    assert torch.equal(onorm.gated_residual_fp32(x, y, one.bfloat16()), x + y)
+
+
+def test_gated_residual_matches_fp64_brute_force():
+    x, y, g = _norm_inputs(l=16, c=128)
+    ref = brute.gated_residual(x.double().numpy(), y.double().numpy(), g.double().numpy())
+    got = onorm.gated_residual_fp32(x.float(), y.float(), g.float()).double().numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+    chain = onorm.gated_residual(x, y, g).double().numpy()
+    ref_r = brute.gated_residual(x.double().numpy(), y.double().numpy(), g.double().numpy(),
+                                 round_to=_bf16_round)
+    assert np.mean(chain == ref_r) > 0.999
+    single = onorm.gated_residual_fp32(x, y, g).double().numpy()
+    # One rounding vs two: the single-rounding form is closer to the exact sum.
+    assert np.abs(single - ref).mean() < np.abs(chain - ref).mean()
+
+
+def _planted_unbiased_variance(x, scale, shift, eps):
+    xd = x.double()
+    mean = xd.mean(-1, keepdim=True)
+    var = (xd - mean).pow(2).sum(-1, keepdim=True) / (xd.shape[-1] - 1)
+    return (xd - mean) / torch.sqrt(var + eps) * (1 + scale) + shift
+
+
+def _planted_gain_without_one(x, scale, shift, eps):
+    return onorm.adaln_modulate_exact(x, scale - 1, shift, eps)
+
+
+def _planted_eps_outside_sqrt(x, scale, shift, eps):
+    xd = x.double()
+    mean = xd.mean(-1, keepdim=True)
+    var = (xd - mean).pow(2).mean(-1, keepdim=True)
+    return (xd - mean) / (torch.sqrt(var) + eps) * (1 + scale) + shift
+
+
+@pytest.mark.parametrize("planted", [_planted_unbiased_variance, _planted_gain_without_one,
+                                     _planted_eps_outside_sqrt])
+def test_adaln_known_answer_catches_planted_mistakes(planted):
+    x, scale, shift, eps, expect = _adaln_known_case()
+    assert not torch.allclose(planted(x, scale, shift, eps), expect, atol=1e-3)

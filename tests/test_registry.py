@@ -72,6 +72,8 @@ def test_gates_do_not_cross():
     ("cache/append", "hip_kv_append_gfx950"),
     ("rope/qk_norm_rope_append", "hip_qk_norm_rope_append_gfx950"),
     ("attention/blockwise_causal_varlen", "hip_blockwise_causal_varlen_gfx950"),
+    ("norm/adaln", "hip_adaln_gfx950"),
+    ("norm/gated_residual", "hip_gated_residual_gfx950"),
 ])
 def test_hip_kernels_registered_specialised(key, name):
     specs = reg._REGISTRY[key]
@@ -99,6 +101,11 @@ def test_no_fallback_on_cpu(cpu):
         ops.qk_norm_rope(q, q, w, w, torch.ones(4, 32), torch.zeros(4, 32))
     with pytest.raises(LookupError, match="no kernel for cache/append"):
         ops.kv_cache_append(torch.zeros(2, 1, 8, 2, 64, dtype=torch.bfloat16), q, q, 0)
+    x = torch.zeros(1, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(LookupError, match="no kernel for norm/adaln"):
+        ops.adaln_modulate(x, x[:, :1], x[:, :1])
+    with pytest.raises(LookupError, match="no kernel for norm/gated_residual"):
+        ops.gated_residual(x, x, x[:, :1])
 
 
 def test_accepts_declines_shapes_the_kernel_does_not_cover(cdna4):
