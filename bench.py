@@ -230,7 +230,8 @@ def run_norm(device, layers: int, reps: int) -> dict:
     (8,192 x 3072), bf16, [1, 1, C] modulation rows as the model passes them.
     Each figure is one launch, event-timed inside a graph of distinct inputs, next to
     the reference's unfused torch expression (``ops/reference/norm.py:20,25``) timed
-    the same way."""
+    the same way, and to torch's own copy and add of the same activation (the
+    streaming rate this GPU reaches at that size with the same read/write mix)."""
     import torch
     import torch.nn.functional as F
 
@@ -268,7 +269,17 @@ def run_norm(device, layers: int, reps: int) -> dict:
                 "bytes": nbytes, "torch_unfused_us": rms * 1e3, "speedup_vs_torch": rms / ms,
                 "shape": [1, rows, cols]}
             del fg, rg
-        del xs, ys, mod, parts
+        # Streaming references at the same size: torch's copy (1 read + 1 write, what
+        # adaLN moves) and add (2 reads + 1 write, what the gated residual moves).
+        zs = [torch.empty_like(x) for x in xs]
+        cg = harness.capture(lambda: [zs[i].copy_(xs[i]) for i in range(n)])
+        cms = harness.event_time_ms(cg.replay, reps=reps) / n
+        ag = harness.capture(lambda: [torch.add(xs[i], ys[i], out=zs[i]) for i in range(n)])
+        ams = harness.event_time_ms(ag.replay, reps=reps) / n
+        out[f"stream_ref_{name}"] = {
+            "copy_us": cms * 1e3, "copy_gbps": 2 * act / (cms * 1e-3) / 1e9,
+            "add_us": ams * 1e3, "add_gbps": 3 * act / (ams * 1e-3) / 1e9}
+        del xs, ys, zs, mod, parts, cg, ag
     return out
 
 
@@ -369,8 +380,8 @@ def main() -> int:
             extra[name] = run_config(name, device, reps)
             print(f"{name} done: {extra[name]['us']:.1f} us", file=sys.stderr, flush=True)
         extra["norm"] = run_norm(device, args.layers, reps=20)
-        print("norm done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["norm"].items()),
-              file=sys.stderr, flush=True)
+        print("norm done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["norm"].items()
+                                        if "us" in v), file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else run_cpu_baseline(head["inputs"], args.cpu_budget)
 
     line = {
