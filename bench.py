@@ -283,6 +283,37 @@ def run_norm(device, layers: int, reps: int) -> dict:
     return out
 
 
+def run_cross(device, layers: int, reps: int) -> dict:
+    """Cross-attention of the C1 chunk (83 queries, 24 heads x 128, bf16) onto the Wan-5B
+    i2v conditioning: 512 text keys and 257 CLIP image keys, each layer with its own
+    context K/V (``models/dreamzero/model.py:234-241``). One call per stream per layer,
+    event-timed inside a graph over the 30 layers."""
+    import torch
+
+    import dexter_amd.ops as ops
+    from dexter_amd.bench import harness
+
+    h, d, lq = 24, 128, 83
+    g = torch.Generator(device=device).manual_seed(0)
+    rnd = lambda *s: torch.randn(*s, device=device, generator=g).to(torch.bfloat16)  # noqa: E731
+    out = {}
+    q = [rnd(1, lq, h, d) for _ in range(layers)]
+    for name, ctx in (("text", 512), ("image", 257)):
+        k = [rnd(1, ctx, h, d) for _ in range(layers)]
+        v = [rnd(1, ctx, h, d) for _ in range(layers)]
+        graph = harness.capture(lambda: [ops.blockwise_causal_attention(q[i], k[i], v[i])
+                                         for i in range(layers)])
+        ms = harness.event_time_ms(graph.replay, reps=reps) / layers
+        flops = 4 * d * lq * ctx * h
+        nbytes = (2 * lq + 2 * ctx) * h * d * 2
+        out[f"cross_{name}_C1"] = {
+            "us": ms * 1e3, "keys": ctx, "tflops": flops / (ms * 1e-3) / 1e12,
+            "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "pct_hbm_peak": 100 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, "bytes": nbytes}
+        del graph, k, v
+    return out
+
+
 def run_cpu_baseline(inp, budget_s: float) -> dict:
     """The torch fp32 oracle on this host's cores, C1 attention per layer (a bounded sample)."""
     import platform as pyplatform
@@ -329,7 +360,7 @@ def main() -> int:
                     help="seconds of CPU work for the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip C2/C3/C4")
-    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm"], default=None,
+    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm", "cross"], default=None,
                     help="time one config's attention only (for profiling runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run a plain device copy of this size (counter calibration)")
@@ -362,8 +393,9 @@ def main() -> int:
         print(f"copy calibration: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
         del src, dst
 
-    if args.only == "norm":
-        res = run_norm(device, args.layers, reps=max(10, args.steps))
+    if args.only in ("norm", "cross"):
+        run = run_norm if args.only == "norm" else run_cross
+        res = run(device, args.layers, reps=max(10, args.steps))
         print(json.dumps({"only": args.only, **res}), flush=True)
         return 0
     if args.only:
@@ -382,6 +414,9 @@ def main() -> int:
         extra["norm"] = run_norm(device, args.layers, reps=20)
         print("norm done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["norm"].items()
                                         if "us" in v), file=sys.stderr, flush=True)
+        extra["cross"] = run_cross(device, args.layers, reps=20)
+        print("cross done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["cross"].items()),
+              file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else run_cpu_baseline(head["inputs"], args.cpu_budget)
 
     line = {

@@ -83,6 +83,7 @@ struct AttnArgs {
   float* ws_ml;    // [partials][bm][2] (exponent reference in log2 units, sum l)
   const void* starts; int starts_i64; int n_blocks;
   int B, H, Lq, Lk;
+  int kv_group;      // query heads per K/V head (grouped-query attention; 1 = one each)
   int causal;
   int n_qtiles;
   int bm;            // queries per work item: 128 (dual-stream decode) or 256 (paired groups)
@@ -547,10 +548,13 @@ struct Coord {
 // Map index i of a range laid out as [groups G][ranks R] with XCD-aware
 // interleaving: when G % 8 == 0, index i runs on XCD i % 8 and all ranks of
 // group g share XCD g % 8.
-__device__ __forceinline__ void split_index(int i, int G, int& gidx, int& rank) {
+__device__ __forceinline__ void split_index(int i, int G, bool contiguous, int& gidx,
+                                            int& rank) {
   if ((G & 7) == 0) {
     const int xcd = i & 7, slot = i >> 3, g8 = G >> 3;
-    gidx = xcd + 8 * (slot % g8);
+    // contiguous: XCD x takes groups [x G/8, (x+1) G/8), so heads that share
+    // a K/V head (adjacent under grouped-query attention) share an L2.
+    gidx = contiguous ? xcd * g8 + slot % g8 : xcd + 8 * (slot % g8);
     rank = slot / g8;
   } else {
     gidx = i % G;
@@ -582,7 +586,7 @@ __device__ __forceinline__ Coord locate(const AttnArgs& a, int idx, bool combine
   }
   const int per_q = combine ? chunks : c.n_splits;
   int gidx, rank;
-  split_index(local, G, gidx, rank);
+  split_index(local, G, a.kv_group > 1, gidx, rank);
   c.split = rank % per_q;
   c.qtile = a.n_qtiles - 1 - rank / per_q;  // heaviest (latest) query tiles first
   if (a.n_seg == 0) {
@@ -926,7 +930,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   // can see (the whole cache and all Lq new keys) so that its tile loads go
   // out before the block starts are read; it skips the tiles past the
   // visible range and masks the straddling ones per key.
-  int kv_min = 0, kv_max = cache_len + a.Lq;
+  int kv_min = 0, kv_max = cache_len + a.Lk;
   if (NS == 1) {
     kv_min = cache_len + visible_end(a, q0);
     kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
@@ -945,11 +949,12 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   src.n_ct = n_ct;
   {
     const int rows_c = min(cache_len, kv_max), rows_n = kv_max - cache_len;
-    const int64_t coff = b * a.c_sb + h * a.c_sh;
+    const int hk = a.kv_group == 1 ? h : h / a.kv_group;  // K/V head of this query head
+    const int64_t coff = b * a.c_sb + hk * a.c_sh;
     src.kc = make_rsrc(a.ck ? a.ck + coff : a.q, rows_c, src.c_ss2, D);
     src.vc = make_rsrc(a.cv ? a.cv + coff : a.q, rows_c, src.c_ss2, D);
-    src.kn = make_rsrc(a.k + b * a.k_sb + h * a.k_sh, rows_n, src.k_sl2, D);
-    src.vn = make_rsrc(a.v + b * a.v_sb + h * a.v_sh, rows_n, src.v_sl2, D);
+    src.kn = make_rsrc(a.k + b * a.k_sb + hk * a.k_sh, rows_n, src.k_sl2, D);
+    src.vn = make_rsrc(a.v + b * a.v_sb + hk * a.v_sh, rows_n, src.v_sl2, D);
     src.none = make_rsrc(a.q, 0, 0, D);
   }
 
@@ -1349,11 +1354,12 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   src.n_ct = n_ct;
   {
     const int rows_c = min(cache_len, kv_max), rows_n = kv_max - cache_len;
-    const int64_t coff = b * a.c_sb + h * a.c_sh;
+    const int hk = a.kv_group == 1 ? h : h / a.kv_group;  // K/V head of this query head
+    const int64_t coff = b * a.c_sb + hk * a.c_sh;
     src.kc = make_rsrc(a.ck ? a.ck + coff : a.q, rows_c, src.c_ss2, D);
     src.vc = make_rsrc(a.cv ? a.cv + coff : a.q, rows_c, src.c_ss2, D);
-    src.kn = make_rsrc(a.k + b * a.k_sb + h * a.k_sh, rows_n, src.k_sl2, D);
-    src.vn = make_rsrc(a.v + b * a.v_sb + h * a.v_sh, rows_n, src.v_sl2, D);
+    src.kn = make_rsrc(a.k + b * a.k_sb + hk * a.k_sh, rows_n, src.k_sl2, D);
+    src.vn = make_rsrc(a.v + b * a.v_sb + hk * a.v_sh, rows_n, src.v_sl2, D);
     src.none = make_rsrc(a.q, 0, 0, D);
   }
 
@@ -1666,12 +1672,12 @@ int choose_uniform_splits(int64_t units, int64_t Lq, int64_t tiles, int cus, int
                                                      std::max<int64_t>(tiles, 1)})));
 }
 
-Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
+Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t cache_len,
                const int64_t* cache_lens) {
   Plan p{};
   const int cus = device_cus();
   if (!cache_lens) {
-    const int64_t tiles = cdiv(cache_len, kBN) + cdiv(Lq, kBN);
+    const int64_t tiles = cdiv(cache_len, kBN) + cdiv(Lk, kBN);
     p.uniform_splits = choose_uniform_splits(B * H, Lq, tiles, cus, p.streams);
     p.bm = bm_of(p.streams);
     p.n_qtiles = int(cdiv(Lq, p.bm));
@@ -1690,7 +1696,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t H, int64_t D, int64_t cache_len,
     std::vector<int64_t> tiles(B);
     int64_t total = 0;
     for (int i = 0; i < int(B); ++i) {
-      tiles[i] = cdiv(cache_lens[i], kBN) + cdiv(Lq, kBN);
+      tiles[i] = cdiv(cache_lens[i], kBN) + cdiv(Lk, kBN);
       total += tiles[i];
     }
     // Dual-stream decode items (128 queries, one workgroup per CU) when that
@@ -1789,17 +1795,23 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                     int64_t v_sl, int64_t v_sh, const void* cache, int64_t c_plane,
                     int64_t c_sb, int64_t c_ss, int64_t c_sh, void* out, int64_t o_sb,
                     int64_t o_sl, int64_t o_sh, int dtype, int64_t B, int64_t Lq, int64_t Lk,
-                    int64_t H, int64_t D, int64_t cache_len, const int64_t* cache_lens,
+                    int64_t H, int64_t Hkv, int64_t D, int64_t cache_len,
+                    const int64_t* cache_lens,
                     const void* starts, int starts_dtype, int64_t n_blocks, int causal,
                     float softmax_scale, void* workspace, int64_t ws_bytes, void* stream) {
   DX_CHECK_ARG(dtype == DX_BF16 || dtype == DX_F16,
                "attention: dtype code %d unsupported (bf16 or f16)", dtype);
   DX_CHECK_ARG(D == 64 || D == 128, "attention: head_dim %lld unsupported (64 or 128)",
                (long long)D);
-  DX_CHECK_ARG(B >= 0 && Lq >= 0 && H > 0, "attention: bad shape");
-  DX_CHECK_ARG(Lk == Lq,
-               "attention: k/v length %lld must equal q length %lld (the block mask is "
-               "[q_len, cache_len + q_len])",
+  DX_CHECK_ARG(B >= 0 && Lq >= 0 && Lk >= 0 && H > 0, "attention: bad shape");
+  DX_CHECK_ARG(Hkv > 0 && H % Hkv == 0,
+               "attention: %lld query heads are not a multiple of %lld k/v heads", (long long)H,
+               (long long)Hkv);
+  // Lk != Lq is cross-attention: every key visible, no block or causal mask
+  // (a block or causal mask is defined on the [q_len, cache_len + q_len] grid).
+  DX_CHECK_ARG(Lk == Lq || (n_blocks == 0 && !causal),
+               "attention: k/v length %lld must equal q length %lld with block_boundaries or "
+               "causal (the block mask is [q_len, cache_len + q_len])",
                (long long)Lk, (long long)Lq);
   DX_CHECK_ARG(n_blocks >= 0 && (n_blocks == 0 || starts),
                "attention: block_boundaries pointer missing");
@@ -1818,7 +1830,8 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   }
   DX_CHECK_ARG(max_cache >= 0, "attention: negative cache_len");
   DX_CHECK_ARG(max_cache == 0 || cache, "attention: cache_len > 0 needs a cache");
-  DX_CHECK_ARG(max_cache + Lq < (int64_t(1) << 30), "attention: sequence too long");
+  DX_CHECK_ARG(max_cache + std::max(Lq, Lk) < (int64_t(1) << 30), "attention: sequence too long");
+  DX_CHECK_ARG(Lk > 0 || max_cache > 0 || Lq == 0, "attention: no keys to attend to");
   DX_CHECK_ARG(q && k && v && out, "attention: null pointer");
   DX_CHECK_ARG(al16(q) && al16(k) && al16(v) && al16(out) && (!cache || al16(cache)),
                "attention: pointers must be 16-byte aligned");
@@ -1830,14 +1843,14 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                "attention: strides must be multiples of 8 elements");
   {
     // Key/value rows are addressed with 32-bit byte offsets per (batch, head).
-    const int64_t rows = max_cache + Lq;
+    const int64_t rows = max_cache + Lk;
     const int64_t stride = std::max({cache ? c_ss : int64_t(0), k_sl, v_sl});
     DX_CHECK_ARG(rows * stride * 2 < (int64_t(1) << 31),
                  "attention: %lld rows of stride %lld exceed 32-bit offsets", (long long)rows,
                  (long long)stride);
   }
   if (B * Lq == 0) return DX_OK;
-  const Plan p = make_plan(B, Lq, H, D, cache_len, cache_lens);
+  const Plan p = make_plan(B, Lq, Lk, H, D, cache_len, cache_lens);
   DX_CHECK_ARG(p.items < (int64_t(1) << 31), "attention: grid too large");
   if (p.ws_bytes > 0) {
     if (!workspace || ws_bytes < p.ws_bytes) {
@@ -1859,6 +1872,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.bm * D) : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
   a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);
+  a.kv_group = int(H / Hkv);
   a.causal = causal != 0;
   a.n_qtiles = p.n_qtiles;
   a.bm = p.bm;
@@ -1906,13 +1920,13 @@ extern "C" int dx_blockwise_causal_attention(
     int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
     const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh, void* out,
     int64_t o_sb, int64_t o_sl, int64_t o_sh, int dtype, int64_t B, int64_t Lq, int64_t Lk,
-    int64_t H, int64_t D, int64_t cache_len, const void* block_starts, int starts_dtype,
-    int64_t n_blocks, int causal, float softmax_scale, void* workspace,
+    int64_t H, int64_t Hkv, int64_t D, int64_t cache_len, const void* block_starts,
+    int starts_dtype, int64_t n_blocks, int causal, float softmax_scale, void* workspace,
     int64_t workspace_bytes, void* stream) {
   return attention_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache,
                          c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
-                         D, cache_len, nullptr, block_starts, starts_dtype, n_blocks, causal,
-                         softmax_scale, workspace, workspace_bytes, stream);
+                         Hkv, D, cache_len, nullptr, block_starts, starts_dtype, n_blocks,
+                         causal, softmax_scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dx_blockwise_causal_attention_varlen(
@@ -1920,20 +1934,20 @@ extern "C" int dx_blockwise_causal_attention_varlen(
     int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
     const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh, void* out,
     int64_t o_sb, int64_t o_sl, int64_t o_sh, int dtype, int64_t B, int64_t Lq, int64_t Lk,
-    int64_t H, int64_t D, const int64_t* cache_lens, const void* block_starts,
+    int64_t H, int64_t Hkv, int64_t D, const int64_t* cache_lens, const void* block_starts,
     int starts_dtype, int64_t n_blocks, int causal, float softmax_scale, void* workspace,
     int64_t workspace_bytes, void* stream) {
   DX_CHECK_ARG(cache_lens != nullptr, "attention varlen: cache_lens is null");
   return attention_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache,
                          c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
-                         D, 0, cache_lens, block_starts, starts_dtype, n_blocks, causal,
+                         Hkv, D, 0, cache_lens, block_starts, starts_dtype, n_blocks, causal,
                          softmax_scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
                                                 int64_t D, int64_t cache_len,
                                                 const int64_t* cache_lens) {
-  if (B < 0 || Lq < 0 || H <= 0 || (D != 64 && D != 128) || cache_len < 0 || Lk != Lq ||
+  if (B < 0 || Lq < 0 || Lk < 0 || H <= 0 || (D != 64 && D != 128) || cache_len < 0 ||
       (cache_lens && B > kMaxSeg)) {
     set_error("attention_workspace_bytes: bad shape");
     return -DX_EINVAL;
@@ -1945,5 +1959,5 @@ extern "C" int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t L
         return -DX_EINVAL;
       }
   if (B * Lq == 0) return 0;
-  return make_plan(B, Lq, H, D, cache_len, cache_lens).ws_bytes;
+  return make_plan(B, Lq, Lk, H, D, cache_len, cache_lens).ws_bytes;
 }

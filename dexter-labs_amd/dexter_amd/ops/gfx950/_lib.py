@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -65,7 +65,7 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         _p, _l, _l, _l,            # v
         _p, _l, _l, _l, _l,        # cache, plane, sb, ss, sh
         _p, _l, _l, _l,            # out
-        _i, _l, _l, _l, _l, _l,    # dtype, B, Lq, Lk, H, D
+        _i, _l, _l, _l, _l, _l, _l,  # dtype, B, Lq, Lk, H, Hkv, D
         _l, _p, _i, _l,            # cache_len, starts, starts dtype, n_blocks
         _i, _f,                    # causal, scale
         _p, _l, _p]),              # workspace, bytes, stream
@@ -75,7 +75,7 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         _p, _l, _l, _l,
         _p, _l, _l, _l, _l,
         _p, _l, _l, _l,
-        _i, _l, _l, _l, _l, _l,
+        _i, _l, _l, _l, _l, _l, _l,
         ctypes.POINTER(ctypes.c_int64), _p, _i, _l,
         _i, _f,
         _p, _l, _p]),

@@ -18,6 +18,19 @@ Differences from the Triton wrapper it replaces, none visible in results:
 Semantics follow the torch reference op (the correctness oracle): a query with
 no visible key gives NaN (the reference's softmax of an all ``-inf`` row);
 ``block_boundaries`` rows before the first start see only the cache.
+
+Two cases the reference op cannot take are defined as its callers use them:
+
+* **Cross-attention.** ``k``/``v`` longer or shorter than ``q`` with no block
+  boundaries and ``causal=False``: every key is visible. ``CrossAttention``
+  calls the op so for the text and image conditioning
+  (``models/dreamzero/model.py:234-241``); the reference's mask is
+  ``[q_len, cache_len + q_len]`` (``ops/reference/attention.py:30``) and the
+  Triton limits ignore keys past ``q_len`` (``blockwise_causal.py:134-135``).
+* **Grouped-query attention.** ``k``/``v`` (and the cache) with ``Hkv`` heads,
+  ``H`` a multiple of ``Hkv``: query head ``h`` reads K/V head ``h // (H // Hkv)``,
+  what ``repeat_interleave(H // Hkv, dim=2)`` gives
+  (``vla/groot/backbone.py:109-114``), without materialising the copy.
 """
 
 from __future__ import annotations
@@ -35,7 +48,8 @@ def _accepts(q, k, v, *args, **kwargs) -> bool:
     return (q.is_cuda and q.dtype in MATRIX_DTYPES and q.dim() == 4
             and k.dtype == q.dtype and v.dtype == q.dtype
             and k.shape == v.shape and k.dim() == 4
-            and q.shape[-1] in (64, 128) and k.shape[-1] == q.shape[-1])
+            and q.shape[-1] in (64, 128) and k.shape[-1] == q.shape[-1]
+            and k.shape[2] > 0 and q.shape[2] % k.shape[2] == 0)
 
 
 def _starts(block_boundaries, q_len: int, device: torch.device):
@@ -72,19 +86,21 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
     if q.dim() != 4 or k.shape != v.shape or k.dim() != 4:
         raise ValueError("q, k, v must be [B, L, H, D] with k and v of one shape")
     b, q_len, heads, dim = q.shape
-    if k.shape[0] != b or k.shape[2:] != q.shape[2:]:
-        raise ValueError(f"k/v {tuple(k.shape)} do not match q {tuple(q.shape)}")
-    if k.shape[1] != q_len:
+    kv_len, kv_heads = k.shape[1], k.shape[2]
+    if k.shape[0] != b or k.shape[3] != dim or kv_heads == 0 or heads % kv_heads:
+        raise ValueError(f"k/v {tuple(k.shape)} do not match q {tuple(q.shape)} (the k/v heads "
+                         "must divide the query heads)")
+    if kv_len != q_len and (block_boundaries is not None or causal):
         raise ValueError(
-            f"k/v length {k.shape[1]} must equal q length {q_len}: the block mask is "
-            f"[q_len, cache_len + q_len] (ops/reference/attention.py:30)")
+            f"k/v length {kv_len} must equal q length {q_len} with block_boundaries or causal: "
+            f"the block mask is [q_len, cache_len + q_len] (ops/reference/attention.py:30)")
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(dim)
     q, k, v = as_rows(q), as_rows(k), as_rows(v)
     max_cache = max(cache_lens) if cache_lens is not None else cache_len
     if max_cache > 0:
         if kv_cache is None:
             raise ValueError("cache_len > 0 needs kv_cache")
-        _check_cache(kv_cache, b, heads, dim, q.dtype, max_cache)
+        _check_cache(kv_cache, b, kv_heads, dim, q.dtype, max_cache)
         cache_ptr = kv_cache.data_ptr()
         c_strides = [kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2),
                      kv_cache.stride(3)]
@@ -96,14 +112,16 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
     arr = None
     if cache_lens is not None:
         arr = (_lib.ctypes.c_int64 * b)(*[int(x) for x in cache_lens])
-    ws_bytes = lib.dx_attention_workspace_bytes(b, q_len, q_len, heads, dim, int(cache_len), arr)
+    if kv_len == 0 and max_cache == 0 and q_len > 0:
+        raise ValueError("attention over no keys: k/v are empty and there is no cache")
+    ws_bytes = lib.dx_attention_workspace_bytes(b, q_len, kv_len, heads, dim, int(cache_len), arr)
     if ws_bytes < 0:
         _lib.check(-ws_bytes, "attention workspace")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     common = [
         q.data_ptr(), *strides(q, 3), k.data_ptr(), *strides(k, 3), v.data_ptr(), *strides(v, 3),
         cache_ptr, *c_strides, out.data_ptr(), *strides(out, 3),
-        _lib.dtype_code(q.dtype), b, q_len, q_len, heads, dim,
+        _lib.dtype_code(q.dtype), b, q_len, kv_len, heads, kv_heads, dim,
     ]
     tail = [_lib.ptr(starts), starts_dt, n_blocks, int(bool(causal)), float(scale),
             _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device)]

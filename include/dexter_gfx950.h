@@ -65,7 +65,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 3
+#define DX_ABI_VERSION 4
 
 /*
  * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.
@@ -128,9 +128,15 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  *     n_blocks == 0        : Lk (one block: every current key)
  *     otherwise            : the largest block end among blocks [s_b, s_{b+1})
  *                            (last end = Lq) containing i; 0 if none does
- *   (ops/reference/attention.py:22-47). Lk must equal Lq, as the reference's
- *   mask shape requires. A query with no visible key yields NaN, as the
- *   reference's softmax over an all -inf row does.
+ *   (ops/reference/attention.py:22-47). With causal or block starts Lk must
+ *   equal Lq, as the reference's mask shape requires. Lk != Lq with
+ *   n_blocks == 0 and causal == 0 is cross-attention: every key visible (the
+ *   reference's mask cannot take it, attention.py:30; the model calls it so,
+ *   models/dreamzero/model.py:234-241). A query with no visible key yields NaN,
+ *   as the reference's softmax over an all -inf row does.
+ * Grouped-query attention: q has H heads, k, v and the cache Hkv heads, H a
+ *   multiple of Hkv; query head h reads K/V head h / (H / Hkv), the head that
+ *   k.repeat_interleave(H / Hkv, dim=2) would put at h (vla/groot/backbone.py:109-114).
  * block_starts: device pointer to n_blocks int32 (starts_dtype DX_I32) or
  * int64 (DX_I64) block start indices, read on the device (no host sync),
  * sorted ascending (the reference builds them with torch.arange).
@@ -148,7 +154,7 @@ int dx_blockwise_causal_attention(
     const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
     const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
     void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
-    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D,
+    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t Hkv, int64_t D,
     int64_t cache_len, const void* block_starts, int starts_dtype, int64_t n_blocks,
     int causal, float softmax_scale,
     void* workspace, int64_t workspace_bytes, void* stream);
@@ -164,7 +170,7 @@ int dx_blockwise_causal_attention_varlen(
     const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
     const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
     void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
-    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D,
+    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t Hkv, int64_t D,
     const int64_t* cache_lens, const void* block_starts, int starts_dtype,
     int64_t n_blocks, int causal, float softmax_scale,
     void* workspace, int64_t workspace_bytes, void* stream);

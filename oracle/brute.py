@@ -36,9 +36,12 @@ def key_visible(i: int, j: int, q_len: int, cache_len: int, starts, causal: bool
 
 def attention(q, k, v, cache_k=None, cache_v=None, cache_len=0, starts=None,
               causal=False, scale=None):
-    """q/k/v: arrays ``[B, L, H, D]``; cache_k/v ``[B, S, H, D]``. Returns fp64 ``[B, L, H, D]``.
+    """q ``[B, Lq, H, D]``, k/v ``[B, Lk, Hkv, D]``; cache_k/v ``[B, S, Hkv, D]``.
+    Returns fp64 ``[B, Lq, H, D]``.
 
     A query with no visible key gives NaN (0/0), as a softmax over nothing.
+    With ``Hkv < H`` query head ``hh`` reads k/v head ``hh // (H // Hkv)``.
+    ``Lk != Lq`` is meant without a mask (every key visible).
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -52,17 +55,20 @@ def attention(q, k, v, cache_k=None, cache_v=None, cache_len=0, starts=None,
     else:
         keys, vals = k, v
     n_keys = keys.shape[1]
+    group = h // keys.shape[2]  # query heads per k/v head
     out = np.empty((b, q_len, h, d), dtype=np.float64)
     for i in range(q_len):
-        vis = np.array([key_visible(i, j, q_len, cache_len, starts, causal) for j in range(n_keys)])
+        vis = np.array([key_visible(i, j, q_len, cache_len, starts, causal) for j in range(n_keys)],
+                       dtype=bool)
         for bb in range(b):
             for hh in range(h):
                 if not vis.any():
                     out[bb, i, hh] = np.nan
                     continue
-                s = keys[bb, vis, hh] @ q[bb, i, hh] * scale
+                kh = hh // group
+                s = keys[bb, vis, kh] @ q[bb, i, hh] * scale
                 w = np.exp(s - s.max())
-                out[bb, i, hh] = (w[:, None] * vals[bb, vis, hh]).sum(0) / w.sum()
+                out[bb, i, hh] = (w[:, None] * vals[bb, vis, kh]).sum(0) / w.sum()
     return out
 
 

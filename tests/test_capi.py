@@ -78,14 +78,23 @@ def test_bad_arguments_are_rejected(built_lib):
                           99, 1, 1, 2, 64, 8, 0, None)
     assert rc == _lib.DX_EINVAL and "dtype" in lib.dx_last_error().decode()
     args = [16, 0, 0, 0] * 3 + [None, 0, 0, 0, 0] + [16, 0, 0, 0]
-    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 8, 2, 96, 0, None,
+    # (dtype, B, Lq, Lk, H, Hkv, D, cache_len, starts, starts dtype, n_blocks, causal, scale,
+    #  workspace, bytes, stream)
+    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 8, 2, 2, 96, 0, None,
                                            _lib.DX_I32, 0, 0, 1.0, None, 0, None)
     assert rc == _lib.DX_EINVAL and "head_dim 96" in lib.dx_last_error().decode()
-    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 9, 2, 128, 0, None,
-                                           _lib.DX_I32, 0, 0, 1.0, None, 0, None)
+    # Lk != Lq is cross-attention, defined only without a causal or block mask.
+    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 9, 2, 2, 128, 0, None,
+                                           _lib.DX_I32, 0, 1, 1.0, None, 0, None)
     assert rc == _lib.DX_EINVAL and "must equal q length" in lib.dx_last_error().decode()
     with pytest.raises(ValueError, match="must equal q length"):
         _lib.check(rc, "attention")
+    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 8, 6, 4, 128, 0, None,
+                                           _lib.DX_I32, 0, 0, 1.0, None, 0, None)
+    assert rc == _lib.DX_EINVAL and "not a multiple" in lib.dx_last_error().decode()
+    rc = lib.dx_blockwise_causal_attention(*args, _lib.DX_BF16, 1, 8, 0, 2, 2, 128, 0, None,
+                                           _lib.DX_I32, 0, 0, 1.0, None, 0, None)
+    assert rc == _lib.DX_EINVAL and "no keys" in lib.dx_last_error().decode()
 
 
 def test_norm_entry_points_validate_before_any_launch(built_lib):

@@ -282,11 +282,15 @@ def test_varlen_matches_per_sequence_calls(device, built_lib):
         assert_parity(one, ref)
 
 
-def test_kv_length_mismatch_is_an_error(device, built_lib):
+def test_kv_length_mismatch_with_a_mask_is_an_error(device, built_lib):
+    """Lk != Lq is cross-attention (every key visible); with a causal or block
+    mask it has no meaning (the mask is [q_len, cache_len + q_len]) and raises."""
     q = torch.zeros(1, 8, 2, 64, dtype=DT, device=device)
     k = torch.zeros(1, 9, 2, 64, dtype=DT, device=device)
     with pytest.raises(ValueError, match="must equal q length"):
-        ops.blockwise_causal_attention(q, k, k)
+        ops.blockwise_causal_attention(q, k, k, causal=True)
+    with pytest.raises(ValueError, match="must equal q length"):
+        ops.blockwise_causal_attention(q, k, k, block_boundaries=torch.tensor([0, 4]))
 
 
 def test_default_scale(device, built_lib):

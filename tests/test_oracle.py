@@ -177,6 +177,68 @@ def test_output_dtype_follows_q():
     assert oatt.blockwise_causal_attention(q, q, q, keep_fp32=True).dtype == torch.float32
 
 
+# ------------------------------------------ cross-attention and GQA -----
+
+def _cross_inputs(seed=3, b=2, lq=7, lk=19, h=4, hkv=4, d=16):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, lq, h, d, generator=g)
+    k = torch.randn(b, lk, hkv, d, generator=g)
+    v = torch.randn(b, lk, hkv, d, generator=g)
+    return q, k, v
+
+
+@pytest.mark.parametrize("lk", [1, 5, 19, 70])
+def test_cross_attention_matches_brute_force_and_sdpa(lk):
+    """kv_len != q_len without a mask: every key visible, against the fp64 brute force
+    and torch's scaled_dot_product_attention with no mask."""
+    q, k, v = _cross_inputs(lk=lk)
+    got = oatt.blockwise_causal_attention(q, k, v, keep_fp32=True)
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy())
+    np.testing.assert_allclose(got.numpy(), ref, rtol=1e-5, atol=1e-5)
+    sd = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    torch.testing.assert_close(got, sd.transpose(1, 2), rtol=1e-5, atol=1e-5)
+
+
+def test_cross_attention_with_cache_sees_cache_then_keys():
+    q, k, v = _cross_inputs(lk=11)
+    cache = torch.randn(2, 2, 9, 4, 16)
+    got = oatt.blockwise_causal_attention(q, k, v, cache, 6, keep_fp32=True)
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy(), cache[0].numpy(), cache[1].numpy(), 6)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_cross_attention_refuses_a_mask():
+    q, k, v = _cross_inputs(lk=9)
+    with pytest.raises(ValueError):
+        oatt.blockwise_causal_attention(q, k, v, causal=True)
+    with pytest.raises(ValueError):
+        oatt.blockwise_causal_attention(q, k, v, block_boundaries=torch.tensor([0, 4]))
+
+
+@pytest.mark.parametrize("hkv", [1, 2])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_matches_brute_force_and_sdpa(hkv, causal):
+    """k/v heads shared by H/Hkv query heads: fp64 brute force (explicit head index)
+    and sdpa(enable_gqa=True)."""
+    q, k, v = _cross_inputs(lk=7, h=4, hkv=hkv)
+    got = oatt.blockwise_causal_attention(q, k, v, causal=causal, keep_fp32=True)
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy(), causal=causal)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=1e-5, atol=1e-5)
+    sd = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                        is_causal=causal, enable_gqa=True)
+    torch.testing.assert_close(got, sd.transpose(1, 2), rtol=1e-5, atol=1e-5)
+
+
+def test_gqa_head_map_is_interleaved_not_tiled():
+    """Query head h reads k/v head h // (H/Hkv) (repeat_interleave), not h % Hkv
+    (repeat): a planted tiling fails the brute force."""
+    q, k, v = _cross_inputs(lk=7, h=4, hkv=2)
+    ref = brute.attention(q.numpy(), k.numpy(), v.numpy())
+    tiled = oatt.blockwise_causal_attention(q, k.repeat(1, 1, 2, 1), v.repeat(1, 1, 2, 1),
+                                            keep_fp32=True)
+    assert not np.allclose(tiled.numpy(), ref, atol=1e-3)
+
+
 # ---------------------------------------------------------------- rope -----
 
 def _bf16_round(x: np.ndarray) -> np.ndarray:
