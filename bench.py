@@ -129,6 +129,27 @@ def run_headline(args, device):
                                                           sin) for i in range(L)])
     pro_ms = harness.event_time_ms(pro_graph.replay, reps=max(5, args.steps // 2)) / L
 
+    # The same step with the cache length read from device memory (a graph
+    # captured once and replayed as the cache grows), per step.
+    cursor = torch.tensor([c], dtype=torch.int32, device=device)
+
+    def step_dev():
+        for layer in range(L):
+            qi, ki, vi = chunk[layer]
+            qc, kc = ops.qk_norm_rope(qi, ki, qw, kw, cos, sin)
+            ops.blockwise_causal_attention(qc, kc, vi, kv_cache=caches[layer], cache_len=cursor)
+
+    dev_graph = harness.capture(step_dev)
+    for _ in range(args.warmup):
+        dev_graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dev_graph.replay()
+    torch.cuda.synchronize()
+    dev_ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    del dev_graph
+
     # Fused prologue + append (the priming pass's form), per launch.
     def prime():
         for i in range(L):
@@ -148,6 +169,7 @@ def run_headline(args, device):
         "ms_per_step": ms_per_step,
         "value": value,
         "eager_ms_per_step": eager_ms,
+        "device_cursor_ms_per_step": dev_ms_per_step,
         "attn_ms": attn_ms,
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
@@ -405,7 +427,9 @@ def main() -> int:
 
     head = run_headline(args, device)
     print(f"headline done: {head['ms_per_step']:.4f} ms/step", file=sys.stderr, flush=True)
-    extra = {"eager_ms_per_step": head["eager_ms_per_step"], "prologue_C1": head["prologue"],
+    extra = {"eager_ms_per_step": head["eager_ms_per_step"],
+             "device_cursor_ms_per_step": head["device_cursor_ms_per_step"],
+             "prologue_C1": head["prologue"],
              "prologue_append_fused_C1": head["prologue_append_fused"]}
     if not args.no_extra:
         for name, reps in (("C2", 20), ("C3", 20), ("C4", 50)):

@@ -96,6 +96,11 @@ struct AttnArgs {
   // blocks [comb_base[i], comb_base[i+1]). n_seg == 0: one uniform segment
   // over all B*H (batch, head) pairs.
   int n_seg;
+  // Device-resident cache length (uniform mode): when set, the kernels read
+  // the cached row count from this int32 at launch, clamped to [0, cache_len]
+  // (cache_len then holds the cache capacity the launch was planned for), so
+  // a captured graph follows the cache as it grows between replays.
+  const int32_t* cache_len_dev;
   int seg_b[kMaxSeg], seg_splits[kMaxSeg], seg_cache[kMaxSeg];
   int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
 };
@@ -106,11 +111,13 @@ struct AttnArgs {
 // otherwise issue one after another.
 __device__ __forceinline__ void prefetch_args(const AttnArgs& a) {
   static_assert(offsetof(AttnArgs, n_seg) < 256, "argument header spans four lines");
+  static_assert(offsetof(AttnArgs, cache_len_dev) / 64 == 4, "device cache length on line five");
   const uint64_t l0 = reinterpret_cast<uint64_t>(a.q);
   const uint64_t l1 = uint64_t(a.v_sb);
   const uint64_t l2 = uint64_t(a.c_sh);
   const uint32_t l3 = uint32_t(a.n_seg);
-  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3));
+  const uint64_t l4 = reinterpret_cast<uint64_t>(a.cache_len_dev);
+  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3), "s"(l4));
 }
 
 template <typename T> struct Mfma;
@@ -571,6 +578,7 @@ __device__ __forceinline__ Coord locate(const AttnArgs& a, int idx, bool combine
     G = a.B * a.H;
     c.n_splits = a.n_splits;
     c.cache_len = a.cache_len;
+    if (a.cache_len_dev) c.cache_len = min(max(*a.cache_len_dev, 0), a.cache_len);
     local = idx;
     seg_item_base = 0;
   } else {
@@ -1796,7 +1804,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                     int64_t c_sb, int64_t c_ss, int64_t c_sh, void* out, int64_t o_sb,
                     int64_t o_sl, int64_t o_sh, int dtype, int64_t B, int64_t Lq, int64_t Lk,
                     int64_t H, int64_t Hkv, int64_t D, int64_t cache_len,
-                    const int64_t* cache_lens,
+                    const int64_t* cache_lens, const int32_t* cache_len_dev,
                     const void* starts, int starts_dtype, int64_t n_blocks, int causal,
                     float softmax_scale, void* workspace, int64_t ws_bytes, void* stream) {
   DX_CHECK_ARG(dtype == DX_BF16 || dtype == DX_F16,
@@ -1886,6 +1894,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   // exactly -- the reference's uniform softmax over the visible keys.
   a.scale_log2 = std::max(fabsf(softmax_scale) * 1.4426950408889634f, FLT_MIN);
   a.cache_len = int(cache_len);
+  a.cache_len_dev = cache_len_dev;
   a.n_splits = p.uniform_splits;
   a.n_seg = p.n_seg;
   for (int i = 0; i < p.n_seg; ++i) {
@@ -1925,8 +1934,28 @@ extern "C" int dx_blockwise_causal_attention(
     int64_t workspace_bytes, void* stream) {
   return attention_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache,
                          c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
-                         Hkv, D, cache_len, nullptr, block_starts, starts_dtype, n_blocks,
-                         causal, softmax_scale, workspace, workspace_bytes, stream);
+                         Hkv, D, cache_len, nullptr, nullptr, block_starts, starts_dtype,
+                         n_blocks, causal, softmax_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dx_blockwise_causal_attention_dev(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k, int64_t k_sb,
+    int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh, void* out,
+    int64_t o_sb, int64_t o_sl, int64_t o_sh, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+    int64_t H, int64_t Hkv, int64_t D, const void* cache_len_dev, int64_t cache_capacity,
+    const void* block_starts, int starts_dtype, int64_t n_blocks, int causal,
+    float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  DX_CHECK_ARG(cache_len_dev != nullptr, "attention: device cache length pointer is null");
+  DX_CHECK_ARG((reinterpret_cast<uintptr_t>(cache_len_dev) & 3u) == 0,
+               "attention: device cache length must be a 4-byte aligned int32");
+  DX_CHECK_ARG(cache_capacity > 0 && cache, "attention: a device cache length needs a cache of "
+               "positive capacity");
+  return attention_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache,
+                         c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
+                         Hkv, D, cache_capacity, nullptr,
+                         static_cast<const int32_t*>(cache_len_dev), block_starts, starts_dtype,
+                         n_blocks, causal, softmax_scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dx_blockwise_causal_attention_varlen(
@@ -1940,8 +1969,8 @@ extern "C" int dx_blockwise_causal_attention_varlen(
   DX_CHECK_ARG(cache_lens != nullptr, "attention varlen: cache_lens is null");
   return attention_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache,
                          c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
-                         Hkv, D, 0, cache_lens, block_starts, starts_dtype, n_blocks, causal,
-                         softmax_scale, workspace, workspace_bytes, stream);
+                         Hkv, D, 0, cache_lens, nullptr, block_starts, starts_dtype, n_blocks,
+                         causal, softmax_scale, workspace, workspace_bytes, stream);
 }
 
 extern "C" int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,

@@ -6,6 +6,11 @@
 // happens before any launch, with the reference's message ("KV cache full").
 // The copy is bit-exact: 16-byte loads and stores, k and v in the same pass,
 // one 16-byte chunk per thread per iteration of a grid-stride loop.
+//
+// dx_kv_append_dev takes the start row from device memory instead (a cursor
+// that a captured graph reads at every replay). The host cannot check it, so
+// the kernel does: a block that would not fit is not written at all, and a
+// status word (if given) is set to 1.
 #include "dx_common.h"
 
 namespace dx {
@@ -18,9 +23,20 @@ struct AppendArgs {
   int64_t start;
   int64_t chunks;            // B * n * H * chunks_per_row
   int n, H, chunks_per_row;  // chunk = 16 bytes of one head row
+  const int32_t* start_dev;  // device start row (overrides start when set)
+  int32_t* status;           // set to 1 when a device start does not fit (may be null)
+  int64_t capacity;
 };
 
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
+  if (a.start_dev) {
+    const int64_t s = *a.start_dev;
+    if (s < 0 || s + a.n > a.capacity) {
+      if (a.status && blockIdx.x == 0 && threadIdx.x == 0) a.status[0] = 1;
+      return;
+    }
+    a.start = s;
+  }
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   for (int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; c < a.chunks; c += stride) {
     int64_t r = c;
@@ -42,19 +58,22 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
 
 using namespace dx;
 
-extern "C" int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
-                            const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
-                            void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
-                            int64_t c_sh, int dtype, int64_t B, int64_t n, int64_t H,
-                            int64_t D, int64_t capacity, int64_t start, void* stream) {
+static int append_entry(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                        const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh, void* cache,
+                        int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh, int dtype,
+                        int64_t B, int64_t n, int64_t H, int64_t D, int64_t capacity,
+                        int64_t start, const int32_t* start_dev, int32_t* status,
+                        void* stream) {
   DX_CHECK_ARG(dtype == DX_BF16 || dtype == DX_F16 || dtype == DX_F32,
                "kv_append: dtype code %d unsupported", dtype);
   DX_CHECK_ARG(B >= 0 && n >= 0 && H > 0 && D > 0 && start >= 0, "kv_append: bad shape");
-  if (start + n > capacity) {
+  if (!start_dev && start + n > capacity) {
     set_error("KV cache full: %lld + %lld > %lld", (long long)start, (long long)n,
               (long long)capacity);
     return DX_EFULL;
   }
+  DX_CHECK_ARG(!start_dev || (reinterpret_cast<uintptr_t>(start_dev) & 3u) == 0,
+               "kv_append: device start must be a 4-byte aligned int32");
   const int64_t es = dtype == DX_F32 ? 4 : 2;
   const int64_t per16 = 16 / es;
   DX_CHECK_ARG(D % per16 == 0, "kv_append: head_dim must fill 16-byte chunks");
@@ -74,6 +93,9 @@ extern "C" int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k
   a.cv = static_cast<uint8_t*>(cache) + c_plane * es;
   a.c_sb = c_sb * es; a.c_ss = c_ss * es; a.c_sh = c_sh * es;
   a.start = start;
+  a.start_dev = start_dev;
+  a.status = status;
+  a.capacity = capacity;
   a.chunks_per_row = int(D / per16);
   a.n = int(n); a.H = int(H);
   a.chunks = B * n * H * a.chunks_per_row;
@@ -83,4 +105,25 @@ extern "C" int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k
                      static_cast<hipStream_t>(stream), a);
   DX_CHECK_LAUNCH("kv_append");
   return DX_OK;
+}
+
+extern "C" int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                            const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+                            void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
+                            int64_t c_sh, int dtype, int64_t B, int64_t n, int64_t H,
+                            int64_t D, int64_t capacity, int64_t start, void* stream) {
+  return append_entry(k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache, c_plane, c_sb, c_ss,
+                      c_sh, dtype, B, n, H, D, capacity, start, nullptr, nullptr, stream);
+}
+
+extern "C" int dx_kv_append_dev(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                                const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+                                void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
+                                int64_t c_sh, int dtype, int64_t B, int64_t n, int64_t H,
+                                int64_t D, int64_t capacity, const void* start_dev,
+                                void* status, void* stream) {
+  DX_CHECK_ARG(start_dev != nullptr, "kv_append: device start pointer is null");
+  return append_entry(k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache, c_plane, c_sb, c_ss,
+                      c_sh, dtype, B, n, H, D, capacity, 0, static_cast<const int32_t*>(start_dev),
+                      static_cast<int32_t*>(status), stream);
 }

@@ -90,6 +90,12 @@ struct RopeArgs {
   uint16_t* ck; uint16_t* cv; int64_t c_sb, c_ss, c_sh; int64_t start;
   int L, H, D;
   float eps;
+  // Device start row (overrides start when set): a block that would not fit
+  // in capacity rows is not written to the cache and *status (if given)
+  // becomes 1; q_out/k_out are written either way.
+  const int32_t* start_dev;
+  int32_t* status;
+  int64_t capacity;
 };
 
 // Touch every 64-byte line of the arguments up front: independent scalar
@@ -220,11 +226,20 @@ __global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
   *reinterpret_cast<u32x4*>(a.k_out + obase + lo) = pk[0];
   *reinterpret_cast<u32x4*>(a.k_out + obase + hi) = pk[1];
   if (APPEND) {
-    const int64_t cbase = b * a.c_sb + (a.start + l) * a.c_ss + h * a.c_sh;
-    *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = pk[0];
-    *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = pk[1];
-    *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = va[0];
-    *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = va[1];
+    int64_t start = a.start;
+    bool fits = true;
+    if (a.start_dev) {
+      start = *a.start_dev;
+      fits = start >= 0 && start + a.L <= a.capacity;
+      if (!fits && a.status && token == 0 && u == 0) a.status[0] = 1;
+    }
+    if (fits) {
+      const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
+      *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = pk[0];
+      *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = pk[1];
+      *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = va[0];
+      *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = va[1];
+    }
   }
 }
 
@@ -304,7 +319,8 @@ static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
                       const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
                       const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
                       void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
-                      int64_t capacity, int64_t start, int64_t B, int64_t L, int64_t H,
+                      int64_t capacity, int64_t start, const int32_t* start_dev,
+                      int32_t* status, int64_t B, int64_t L, int64_t H,
                       int64_t D, float eps, int interleaved, void* stream, bool append) {
   int rc = check_common(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, io_dtype, qw, kw, wdt, cos,
                         cos_sl, sin, sin_sl, tdt, q_out, k_out, B, L, H, D);
@@ -312,7 +328,9 @@ static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
   if (append) {
     DX_CHECK_ARG(cache && v, "qk_norm_rope_append: null cache or v");
     DX_CHECK_ARG(start >= 0, "qk_norm_rope_append: negative start");
-    if (start + L > capacity) {
+    DX_CHECK_ARG(!start_dev || (reinterpret_cast<uintptr_t>(start_dev) & 3u) == 0,
+                 "qk_norm_rope_append: device start must be a 4-byte aligned int32");
+    if (!start_dev && start + L > capacity) {
       set_error("KV cache full: %lld + %lld > %lld", (long long)start, (long long)L,
                 (long long)capacity);
       return DX_EFULL;
@@ -334,6 +352,7 @@ static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
     a.ck = static_cast<uint16_t*>(cache);
     a.cv = static_cast<uint16_t*>(cache) + c_plane;
     a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh; a.start = start;
+    a.start_dev = start_dev; a.status = status; a.capacity = capacity;
   }
   a.L = int(L); a.H = int(H); a.D = int(D); a.eps = eps;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -363,8 +382,8 @@ extern "C" int dx_qk_norm_rope(const void* q, int64_t q_sb, int64_t q_sl, int64_
                                float eps, int interleaved, void* stream) {
   return rope_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, nullptr, 0, 0, 0, io_dtype,
                     q_weight, k_weight, weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype,
-                    q_out, k_out, nullptr, 0, 0, 0, 0, 0, 0, B, L, H, D, eps, interleaved,
-                    stream, false);
+                    q_out, k_out, nullptr, 0, 0, 0, 0, 0, 0, nullptr, nullptr, B, L, H, D, eps,
+                    interleaved, stream, false);
 }
 
 extern "C" int dx_qk_norm_rope_append(
@@ -377,6 +396,22 @@ extern "C" int dx_qk_norm_rope_append(
     float eps, int interleaved, void* stream) {
   return rope_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, io_dtype,
                     q_weight, k_weight, weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype,
-                    q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity, start, B, L, H,
-                    D, eps, interleaved, stream, true);
+                    q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity, start, nullptr,
+                    nullptr, B, L, H, D, eps, interleaved, stream, true);
+}
+
+extern "C" int dx_qk_norm_rope_append_dev(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k, int64_t k_sb,
+    int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    int io_dtype, const void* q_weight, const void* k_weight, int weight_dtype,
+    const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl, int table_dtype,
+    void* q_out, void* k_out, void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
+    int64_t c_sh, int64_t capacity, const void* start_dev, void* status, int64_t B, int64_t L,
+    int64_t H, int64_t D, float eps, int interleaved, void* stream) {
+  DX_CHECK_ARG(start_dev != nullptr, "qk_norm_rope_append: device start pointer is null");
+  return rope_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, io_dtype,
+                    q_weight, k_weight, weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype,
+                    q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity, 0,
+                    static_cast<const int32_t*>(start_dev), static_cast<int32_t*>(status), B, L,
+                    H, D, eps, interleaved, stream, true);
 }

@@ -49,7 +49,9 @@ class SelfAttention(nn.Module):
         k = F.linear(x, self.k.weight, self.k.bias).view(shape)
         v = F.linear(x, self.v.weight, self.v.bias).view(shape)
 
-        cache_len = kv_cache.length if kv_cache is not None else 0
+        # Read before appending; with a device cursor this is the cursor itself,
+        # which the commit after all layers advances.
+        cache_len = kv_cache.cache_len if kv_cache is not None else 0
         if kv_cache is not None and write and fused_append:
             q, k = kv_cache.append_fused(layer, q, k, v, self.q_norm, self.k_norm, cos, sin,
                                          self.eps)

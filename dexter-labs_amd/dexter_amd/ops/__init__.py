@@ -76,7 +76,7 @@ def blockwise_causal_attention(
     v: torch.Tensor,
     *,
     kv_cache: torch.Tensor | None = None,
-    cache_len: int = 0,
+    cache_len: int | torch.Tensor = 0,
     block_boundaries: torch.Tensor | None = None,
     softmax_scale: float | None = None,
     causal: bool = False,
@@ -87,7 +87,11 @@ def blockwise_causal_attention(
     cached history and every current key before the end of its own block.
     ``None`` is one block (all current keys visible); ``causal=True`` is
     token-causal on the current keys. ``kv_cache`` is ``[2, B, S, H, D]``;
-    rows ``[0, cache_len)`` are read in place, never copied.
+    rows ``[0, cache_len)`` are read in place, never copied. ``cache_len`` may
+    be a device cursor (a one-element int32 tensor) that the kernels read when
+    they run, so a captured graph follows a growing cache. ``k``/``v`` of
+    another length than ``q`` (no mask) is cross-attention; ``k``/``v`` with
+    fewer heads is grouped-query attention.
     """
     return select("attention", "blockwise_causal", q, k, v)(
         q, k, v, kv_cache, cache_len, block_boundaries, softmax_scale, causal)
@@ -116,12 +120,16 @@ def blockwise_causal_attention_varlen(
 
 
 def kv_cache_append(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    start: int) -> None:
+                    start: int | torch.Tensor, status: torch.Tensor | None = None) -> None:
     """Write ``k``/``v`` ``[B, n, H, D]`` into rows ``[start, start+n)`` of both planes
     of ``cache`` ``[2, B, S, H, D]``. Raises ``RuntimeError("KV cache full ...")``
     when ``start + n > S``, before anything is launched.
+
+    ``start`` may be a device cursor (a one-element int32 tensor), read by the
+    kernel when it runs; a block that would not fit is then skipped and
+    ``status`` (an int32 tensor, optional) set to 1.
     """
-    return select("cache", "append", cache, k, v)(cache, k, v, start)
+    return select("cache", "append", cache, k, v)(cache, k, v, start, status)
 
 
 def qk_norm_rope_append(
@@ -133,17 +141,18 @@ def qk_norm_rope_append(
     cos: torch.Tensor,
     sin: torch.Tensor,
     cache: torch.Tensor,
-    start: int,
+    start: int | torch.Tensor,
     eps: float = 1e-6,
     interleaved: bool = True,
+    status: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``qk_norm_rope`` and ``kv_cache_append`` of the rotated k and raw v, in one pass.
 
     Same results as ``q, k = qk_norm_rope(...)`` followed by
-    ``kv_cache_append(cache, k, v, start)``.
+    ``kv_cache_append(cache, k, v, start, status)``; ``start`` may be a device cursor.
     """
     return select("rope", "qk_norm_rope_append", q, k, v, cache)(
-        q, k, v, q_weight, k_weight, cos, sin, cache, start, eps, interleaved)
+        q, k, v, q_weight, k_weight, cos, sin, cache, start, eps, interleaved, status)
 
 
 # Importing the implementation package is what populates the registry.

@@ -36,3 +36,16 @@ def as_rows(t: torch.Tensor) -> torch.Tensor:
 def strides(t: torch.Tensor, dims: int) -> list[int]:
     """The first ``dims`` strides; a size-1 dim gets stride 0 (it is never stepped)."""
     return [0 if t.shape[i] == 1 else t.stride(i) for i in range(dims)]
+
+
+def device_cursor(t: torch.Tensor, device: torch.device, what: str) -> torch.Tensor:
+    """A device-resident cache cursor: a one-element int32 tensor on ``device``.
+
+    Kernels read it when they run, so a captured graph follows it as it moves.
+    It is never copied or converted here: the kernels must read the caller's
+    tensor, the one the caller advances.
+    """
+    if t.dtype != torch.int32 or t.numel() != 1 or t.device != device:
+        raise ValueError(f"{what}: a device cursor must be one int32 element on {device}, got "
+                         f"{t.dtype} x {t.numel()} on {t.device}")
+    return t

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -79,6 +79,34 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         ctypes.POINTER(ctypes.c_int64), _p, _i, _l,
         _i, _f,
         _p, _l, _p]),
+    "dx_blockwise_causal_attention_dev": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l, _l,
+        _p, _l, _l, _l,
+        _i, _l, _l, _l, _l, _l, _l,
+        _p, _l,                    # device cache length (int32), cache capacity
+        _p, _i, _l,
+        _i, _f,
+        _p, _l, _p]),
+    "dx_kv_append_dev": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l, _l,
+        _i, _l, _l, _l, _l,
+        _l, _p, _p, _p]),          # capacity, device start (int32), status, stream
+    "dx_qk_norm_rope_append_dev": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _i,
+        _p, _p, _i,
+        _p, _l, _p, _l, _i,
+        _p, _p,
+        _p, _l, _l, _l, _l, _l, _p, _p,  # cache, plane, sb, ss, sh, capacity, start, status
+        _l, _l, _l, _l,
+        _f, _i, _p]),
     "dx_attention_workspace_bytes": (_l, [_l, _l, _l, _l, _l, _l,
                                           ctypes.POINTER(ctypes.c_int64)]),
     "dx_adaln_modulate": (_i, [

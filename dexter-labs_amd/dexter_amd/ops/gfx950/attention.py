@@ -31,6 +31,11 @@ Two cases the reference op cannot take are defined as its callers use them:
   ``H`` a multiple of ``Hkv``: query head ``h`` reads K/V head ``h // (H // Hkv)``,
   what ``repeat_interleave(H // Hkv, dim=2)`` gives
   (``vla/groot/backbone.py:109-114``), without materialising the copy.
+
+``cache_len`` may be a device cursor (one int32 on the device,
+``dx_blockwise_causal_attention_dev``): the kernels read the cached row count
+when they run, clamped to the cache capacity, and the launch is planned for the
+whole capacity. A graph captured once then stays correct as the cache grows.
 """
 
 from __future__ import annotations
@@ -41,7 +46,7 @@ import torch
 
 from ...registry import Priority, register
 from . import _lib
-from ._common import CDNA4, MATRIX_DTYPES, as_rows, strides
+from ._common import CDNA4, MATRIX_DTYPES, as_rows, device_cursor, strides
 
 
 def _accepts(q, k, v, *args, **kwargs) -> bool:
@@ -82,7 +87,7 @@ def _check_cache(kv_cache, b, heads, dim, dtype, need_rows: int):
 
 
 def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_scale,
-            causal):
+            causal, cursor=None):
     if q.dim() != 4 or k.shape != v.shape or k.dim() != 4:
         raise ValueError("q, k, v must be [B, L, H, D] with k and v of one shape")
     b, q_len, heads, dim = q.shape
@@ -96,6 +101,11 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
             f"the block mask is [q_len, cache_len + q_len] (ops/reference/attention.py:30)")
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(dim)
     q, k, v = as_rows(q), as_rows(k), as_rows(v)
+    if cursor is not None:
+        if kv_cache is None:
+            raise ValueError("a device cache_len needs kv_cache")
+        cursor = device_cursor(cursor, q.device, "blockwise_causal_attention cache_len")
+        cache_len = kv_cache.shape[2]  # planned for the capacity; the kernel clamps the cursor
     max_cache = max(cache_lens) if cache_lens is not None else cache_len
     if max_cache > 0:
         if kv_cache is None:
@@ -125,7 +135,10 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
     ]
     tail = [_lib.ptr(starts), starts_dt, n_blocks, int(bool(causal)), float(scale),
             _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device)]
-    if cache_lens is None:
+    if cursor is not None:
+        rc = lib.dx_blockwise_causal_attention_dev(*common, cursor.data_ptr(), int(cache_len),
+                                                   *tail)
+    elif cache_lens is None:
         rc = lib.dx_blockwise_causal_attention(*common, int(cache_len), *tail)
     else:
         rc = lib.dx_blockwise_causal_attention_varlen(*common, arr, *tail)
@@ -137,6 +150,9 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
           capability=CDNA4, priority=Priority.SPECIALISED, accepts=_accepts)
 def blockwise_causal_attention(q, k, v, kv_cache, cache_len, block_boundaries,
                                softmax_scale, causal=False):
+    if isinstance(cache_len, torch.Tensor):
+        return _launch(q, k, v, kv_cache, 0, None, block_boundaries, softmax_scale, causal,
+                       cursor=cache_len)
     cache_len = int(cache_len)
     if cache_len < 0:
         raise ValueError("cache_len must be >= 0")

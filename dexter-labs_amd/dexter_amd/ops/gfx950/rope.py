@@ -10,6 +10,10 @@ long (Wan's QK norm runs before the head split). One workgroup per token.
 ``rope/qk_norm_rope_append`` is the same pass with the rotated k and the raw
 v also written into rows ``[start, start+L)`` of a ``[2, B, S, H, D]`` cache
 (the fused form of ``KVCache.append``, ``models/dreamzero/model.py:53-58``).
+``start`` may be a device cursor (one int32 on the device,
+``dx_qk_norm_rope_append_dev``), read when the kernel runs; a block that would
+not fit is then not written to the cache and ``status`` (optional int32) is set
+to 1, while q and k are still returned.
 """
 
 from __future__ import annotations
@@ -18,7 +22,7 @@ import torch
 
 from ...registry import Priority, register
 from . import _lib
-from ._common import CDNA4, MATRIX_DTYPES, as_rows, strides
+from ._common import CDNA4, MATRIX_DTYPES, as_rows, device_cursor, strides
 
 _TABLE_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 _MAX_PLANE = 256 * 4 * 16
@@ -79,7 +83,7 @@ def qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps, interleaved=True):
 @register("rope", "qk_norm_rope_append", name="hip_qk_norm_rope_append_gfx950",
           capability=CDNA4, priority=Priority.SPECIALISED, accepts=_accepts_append)
 def qk_norm_rope_append(q, k, v, q_weight, k_weight, cos, sin, cache, start, eps,
-                        interleaved=True):
+                        interleaved=True, status=None):
     q, k, qw, kw, c, s, tdt = _prepare(q, k, q_weight, k_weight, cos, sin)
     b, seq, heads, dim = q.shape
     if v.shape != q.shape or v.dtype != q.dtype:
@@ -95,14 +99,20 @@ def qk_norm_rope_append(q, k, v, q_weight, k_weight, cos, sin, cache, start, eps
     q_out = torch.empty((b, seq, heads, dim), device=q.device, dtype=q.dtype)
     k_out = torch.empty_like(q_out)
     lib = _lib.load()
-    rc = lib.dx_qk_norm_rope_append(
-        q.data_ptr(), *strides(q, 3), k.data_ptr(), *strides(k, 3), v.data_ptr(), *strides(v, 3),
-        _lib.dtype_code(q.dtype),
-        qw.data_ptr(), kw.data_ptr(), _lib.dtype_code(qw.dtype),
-        c.data_ptr(), _row_stride(c), s.data_ptr(), _row_stride(s), _lib.dtype_code(tdt),
-        q_out.data_ptr(), k_out.data_ptr(),
-        cache.data_ptr(), cache.stride(0), cache.stride(1), cache.stride(2), cache.stride(3),
-        cache.shape[2], int(start), b, seq, heads, dim,
-        float(eps), int(bool(interleaved)), _lib.stream_handle(q.device))
+    head = [q.data_ptr(), *strides(q, 3), k.data_ptr(), *strides(k, 3), v.data_ptr(),
+            *strides(v, 3), _lib.dtype_code(q.dtype),
+            qw.data_ptr(), kw.data_ptr(), _lib.dtype_code(qw.dtype),
+            c.data_ptr(), _row_stride(c), s.data_ptr(), _row_stride(s), _lib.dtype_code(tdt),
+            q_out.data_ptr(), k_out.data_ptr(),
+            cache.data_ptr(), cache.stride(0), cache.stride(1), cache.stride(2),
+            cache.stride(3), cache.shape[2]]
+    tail = [b, seq, heads, dim, float(eps), int(bool(interleaved)), _lib.stream_handle(q.device)]
+    if isinstance(start, torch.Tensor):
+        start = device_cursor(start, q.device, "qk_norm_rope_append")
+        if status is not None:
+            status = device_cursor(status, q.device, "qk_norm_rope_append status")
+        rc = lib.dx_qk_norm_rope_append_dev(*head, start.data_ptr(), _lib.ptr(status), *tail)
+    else:
+        rc = lib.dx_qk_norm_rope_append(*head, int(start), *tail)
     _lib.check(rc, "qk_norm_rope_append")
     return q_out, k_out

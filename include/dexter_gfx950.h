@@ -19,6 +19,12 @@
  *                            the same with one cache length per sequence; the
  *                            reference has a scalar cache_len only, and a
  *                            ragged batch there is one call per sequence.
+ *   dx_qk_norm_rope_append_dev, dx_kv_append_dev, dx_blockwise_causal_attention_dev
+ *                            the same three with the cache cursor (start row /
+ *                            cached length) read from device memory, so one
+ *                            captured graph serves every control step while
+ *                            the cache grows; the reference captures only
+ *                            cache-free steps (runtime/graph.py:50-74)
  *   dx_adaln_modulate        ops/gfx1151/norm/adaln.py:108-128 (kernel :20-48;
  *                            semantics ops/reference/norm.py:16-20, dispatcher
  *                            ops/__init__.py:39-49)
@@ -65,7 +71,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 4
+#define DX_ABI_VERSION 5
 
 /*
  * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.
@@ -174,6 +180,54 @@ int dx_blockwise_causal_attention_varlen(
     const int64_t* cache_lens, const void* block_starts, int starts_dtype,
     int64_t n_blocks, int causal, float softmax_scale,
     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Device-cursor forms. The cache row count (attention) or start row (appends)
+ * is an int32 in device memory, read by the kernels when they run: a HIP
+ * graph captured once replays correctly after the cursor moves (a captured
+ * torch add_ on the cursor moves it). The host cannot check the cursor, so:
+ *  - attention clamps it to [0, cache_capacity] and is planned (split count,
+ *    workspace) for cache_capacity rows: call dx_attention_workspace_bytes
+ *    with cache_len = cache_capacity;
+ *  - an append whose block would not fit in capacity rows writes no cache row
+ *    and sets *status to 1 (status may be NULL); the prologue still writes
+ *    q_out and k_out.
+ * Otherwise identical to dx_blockwise_causal_attention, dx_kv_append and
+ * dx_qk_norm_rope_append.
+ * Replaces: the cache-free restriction of runtime/graph.py:50-74
+ * (capture_denoise_step), with models/dreamzero/model.py:53-58,166-175.
+ */
+int dx_blockwise_causal_attention_dev(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+    const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+    void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t Hkv, int64_t D,
+    const void* cache_len_dev, int64_t cache_capacity,
+    const void* block_starts, int starts_dtype, int64_t n_blocks,
+    int causal, float softmax_scale,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+int dx_kv_append_dev(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                     const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+                     void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                     int dtype, int64_t B, int64_t n, int64_t H, int64_t D,
+                     int64_t capacity, const void* start_dev, void* status, void* stream);
+
+int dx_qk_norm_rope_append_dev(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                               const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                               const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+                               int io_dtype,
+                               const void* q_weight, const void* k_weight, int weight_dtype,
+                               const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl,
+                               int table_dtype,
+                               void* q_out, void* k_out,
+                               void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss,
+                               int64_t c_sh, int64_t capacity, const void* start_dev,
+                               void* status,
+                               int64_t B, int64_t L, int64_t H, int64_t D,
+                               float eps, int interleaved, void* stream);
 
 /*
  * Workspace bytes the attention entry points need for this shape on the
