@@ -336,6 +336,51 @@ def run_cross(device, layers: int, reps: int) -> dict:
     return out
 
 
+def run_qkv(device, layers: int, reps: int) -> dict:
+    """The C1 chunk's q/k/v projections (83 tokens x 3072 -> 3 x 3072, bf16, with bias)
+    fused with the QK-norm + rotary prologue (``ops.qkv_norm_rope``), each of 30 layers
+    with its own weights, against three ``F.linear`` (hipBLASLt) plus the HIP prologue:
+    the path it replaces (``models/dreamzero/model.py:162-175``)."""
+    import torch
+    import torch.nn.functional as F
+
+    import dexter_amd.ops as ops
+    from dexter_amd.bench import harness
+    from dexter_amd.bench.workloads import rope_table
+
+    c, heads, dim, tokens = 3072, 24, 128, 83
+    g = torch.Generator(device=device).manual_seed(0)
+    rnd = lambda *s: torch.randn(*s, device=device, generator=g).to(torch.bfloat16)  # noqa: E731
+    x = [rnd(1, tokens, c) for _ in range(layers)]
+    w = [[rnd(c, c).mul_(c ** -0.5) for _ in range(3)] for _ in range(layers)]
+    b = [[rnd(c).mul_(0.1) for _ in range(3)] for _ in range(layers)]
+    nq, nk = rnd(c).add_(1.0), rnd(c).add_(1.0)
+    cos, sin = (t.to(device) for t in rope_table(torch.arange(tokens) + 1245, dim))
+
+    def fused():
+        for i in range(layers):
+            ops.qkv_norm_rope(x[i], w[i][0], b[i][0], w[i][1], b[i][1], w[i][2], b[i][2],
+                              nq, nk, cos, sin, heads)
+
+    def unfused():
+        for i in range(layers):
+            q, k, _ = (F.linear(x[i], w[i][j], b[i][j]).view(1, tokens, heads, dim)
+                       for j in range(3))
+            ops.qk_norm_rope(q, k, nq, nk, cos, sin)
+
+    out = {}
+    for name, fn in (("fused", fused), ("linear_x3_plus_prologue", unfused)):
+        graph = harness.capture(fn)
+        out[f"{name}_us"] = harness.event_time_ms(graph.replay, reps=reps) / layers * 1e3
+        del graph
+    wbytes = 3 * c * c * 2
+    out["weight_bytes"] = wbytes
+    out["fused_weight_gbps"] = wbytes / (out["fused_us"] * 1e-6) / 1e9
+    out["fused_pct_hbm_peak"] = 100 * out["fused_weight_gbps"] / PEAK_HBM_GBPS
+    out["speedup"] = out["linear_x3_plus_prologue_us"] / out["fused_us"]
+    return out
+
+
 def run_cpu_baseline(inp, budget_s: float) -> dict:
     """The torch fp32 oracle on this host's cores, C1 attention per layer (a bounded sample)."""
     import platform as pyplatform
@@ -382,7 +427,8 @@ def main() -> int:
                     help="seconds of CPU work for the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip C2/C3/C4")
-    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm", "cross"], default=None,
+    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm", "cross", "qkv"],
+                    default=None,
                     help="time one config's attention only (for profiling runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run a plain device copy of this size (counter calibration)")
@@ -415,8 +461,8 @@ def main() -> int:
         print(f"copy calibration: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
         del src, dst
 
-    if args.only in ("norm", "cross"):
-        run = run_norm if args.only == "norm" else run_cross
+    if args.only in ("norm", "cross", "qkv"):
+        run = {"norm": run_norm, "cross": run_cross, "qkv": run_qkv}[args.only]
         res = run(device, args.layers, reps=max(10, args.steps))
         print(json.dumps({"only": args.only, **res}), flush=True)
         return 0
@@ -438,6 +484,8 @@ def main() -> int:
         extra["norm"] = run_norm(device, args.layers, reps=20)
         print("norm done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["norm"].items()
                                         if "us" in v), file=sys.stderr, flush=True)
+        extra["qkv"] = run_qkv(device, args.layers, reps=20)
+        print(f"qkv done: fused {extra['qkv']['fused_us']:.2f} us", file=sys.stderr, flush=True)
         extra["cross"] = run_cross(device, args.layers, reps=20)
         print("cross done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["cross"].items()),
               file=sys.stderr, flush=True)

@@ -19,11 +19,13 @@
 // (and v for the cache write) -- is issued before the sum-of-squares
 // reduction: one memory round trip, then LDS, then the stores.
 #include "dx_common.h"
+#include "qkv_gemm.h"
 
 namespace dx {
 namespace {
 
-constexpr int kMaxThreads = 1024;  // H*D <= 1024 units * 16 = 16384
+constexpr int kMaxThreads = 1024;     // H*D <= 1024 units * 16 = 16384
+constexpr int kMaxProjThreads = 512;  // projection epilogue: H*D <= 8192
 
 template <typename W> struct Vec8;
 template <> struct Vec8<bf16_t> {
@@ -96,24 +98,90 @@ struct RopeArgs {
   const int32_t* start_dev;
   int32_t* status;
   int64_t capacity;
+  // Projection input (the fused QKV projection's epilogue): instead of q/k/v,
+  // the kernel reads n_part fp32 split-K partial products [n_part][tokens][3 H D]
+  // (q columns, then k, then v), adds the bias rows (may be null), rounds to
+  // the io type -- the projection's output -- and also writes v to v_out.
+  const float* part; int64_t part_split;  // elements between consecutive partials
+  const uint16_t* bias[3];                // q, k, v bias rows [H D], each may be null
+  uint16_t* v_out;
+  int n_part;
 };
 
 // Touch every 64-byte line of the arguments up front: independent scalar
 // loads and one wait, instead of the chain of dependent loads (each a cache
 // miss at kernel start) that the first uses would otherwise issue.
 __device__ __forceinline__ void prefetch_args(const RopeArgs& a) {
-  static_assert(sizeof(RopeArgs) <= 256, "arguments span at most four lines");
+  static_assert(sizeof(RopeArgs) <= 320, "arguments span at most five lines");
   const uint64_t l0 = reinterpret_cast<uint64_t>(a.q);
   const uint64_t l1 = uint64_t(a.v_sb);
   const uint64_t l2 = reinterpret_cast<uint64_t>(a.q_out);
   const uint32_t l3 = uint32_t(a.L);
-  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3));
+  const uint32_t l4 = uint32_t(a.n_part);
+  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3), "s"(l4));
 }
 
-template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND>
-__global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
+// The projection's output for this thread's six 8-element pieces (q, k, v at
+// the lo and hi offsets): the sum of the split-K partials in split order, plus
+// the bias, rounded to IO once. Partials are read two at a time with all
+// twelve loads of a partial issued together, so the pieces share round trips.
+template <typename IO>
+__device__ __forceinline__ void projected(const RopeArgs& a, const float* row, int64_t hd,
+                                          int lo, int hi, int64_t boff, u32x4 (&q)[2],
+                                          u32x4 (&k)[2], u32x4 (&v)[2]) {
+  const int64_t off[6] = {lo, hi, hd + lo, hd + hi, 2 * hd + lo, 2 * hd + hi};
+  f32x4 s[6][2];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    s[i][0] = *reinterpret_cast<const f32x4*>(row + off[i]);
+    s[i][1] = *reinterpret_cast<const f32x4*>(row + off[i] + 4);
+  }
+  for (int p = 1; p < a.n_part; p += 2) {
+    const float* r1 = row + p * a.part_split;
+    const float* r2 = row + min(p + 1, a.n_part - 1) * a.part_split;
+    const bool two = p + 1 < a.n_part;
+    f32x4 t1[6][2], t2[6][2];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      t1[i][0] = *reinterpret_cast<const f32x4*>(r1 + off[i]);
+      t1[i][1] = *reinterpret_cast<const f32x4*>(r1 + off[i] + 4);
+      t2[i][0] = *reinterpret_cast<const f32x4*>(r2 + off[i]);
+      t2[i][1] = *reinterpret_cast<const f32x4*>(r2 + off[i] + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      s[i][0] += t1[i][0];
+      s[i][1] += t1[i][1];
+      if (two) {
+        s[i][0] += t2[i][0];
+        s[i][1] += t2[i][1];
+      }
+    }
+  }
+  u32x4* out[6] = {&q[0], &q[1], &k[0], &k[1], &v[0], &v[1]};
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    float f[8] = {s[i][0][0], s[i][0][1], s[i][0][2], s[i][0][3],
+                  s[i][1][0], s[i][1][1], s[i][1][2], s[i][1][3]};
+    const uint16_t* b = a.bias[i / 2];
+    if (b) {
+      float bf[8];
+      unpack16<IO>(*reinterpret_cast<const u32x4*>(b + boff + (i & 1 ? hi : lo)), bf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] += bf[e];
+    }
+    u32x4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = pack2<IO>(f[2 * j], f[2 * j + 1]);
+    *out[i] = r;
+  }
+}
+
+template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND, bool PROJ,
+          int kThreads>
+__device__ __forceinline__ void prologue_body(const RopeArgs& a) {
   prefetch_args(a);
-  __shared__ float red[2][kMaxThreads / 64];
+  __shared__ float red[2][kThreads / 64];
   const int token = blockIdx.x;  // b * L + l
   const int b = token / a.L, l = token % a.L;
   const int units_per_head = a.D / 16;
@@ -131,20 +199,27 @@ __global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
   u32x4 qa[2] = {}, ka[2] = {}, va[2] = {};
   typename Vec8<W>::raw wq[2] = {}, wk[2] = {};
   typename Vec8<TB>::raw cr = {}, sr = {};
+  if (active && PROJ) {
+    const int64_t hd = int64_t(a.H) * a.D;
+    const float* row = a.part + int64_t(token) * 3 * hd + h * a.D;
+    projected<IO>(a, row, hd, lo, hi, h * a.D, qa, ka, va);
+  }
   if (active) {
-    const uint16_t* qp = a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh;
-    qa[0] = *reinterpret_cast<const u32x4*>(qp + lo);
-    qa[1] = *reinterpret_cast<const u32x4*>(qp + hi);
-    ka[0] = *reinterpret_cast<const u32x4*>(kp + lo);
-    ka[1] = *reinterpret_cast<const u32x4*>(kp + hi);
+    if (!PROJ) {
+      const uint16_t* qp = a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh;
+      const uint16_t* kp = a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh;
+      qa[0] = *reinterpret_cast<const u32x4*>(qp + lo);
+      qa[1] = *reinterpret_cast<const u32x4*>(qp + hi);
+      ka[0] = *reinterpret_cast<const u32x4*>(kp + lo);
+      ka[1] = *reinterpret_cast<const u32x4*>(kp + hi);
+    }
     wq[0] = Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + lo);
     wq[1] = Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + hi);
     wk[0] = Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + lo);
     wk[1] = Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + hi);
     cr = Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0);
     sr = Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0);
-    if (APPEND) {
+    if (APPEND && !PROJ) {
       const uint16_t* vp = a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
       va[0] = *reinterpret_cast<const u32x4*>(vp + lo);
       va[1] = *reinterpret_cast<const u32x4*>(vp + hi);
@@ -225,6 +300,10 @@ __global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
   *reinterpret_cast<u32x4*>(a.q_out + obase + hi) = pq[1];
   *reinterpret_cast<u32x4*>(a.k_out + obase + lo) = pk[0];
   *reinterpret_cast<u32x4*>(a.k_out + obase + hi) = pk[1];
+  if (PROJ) {
+    *reinterpret_cast<u32x4*>(a.v_out + obase + lo) = va[0];
+    *reinterpret_cast<u32x4*>(a.v_out + obase + hi) = va[1];
+  }
   if (APPEND) {
     int64_t start = a.start;
     bool fits = true;
@@ -243,9 +322,30 @@ __global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
   }
 }
 
+template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND>
+__global__ __launch_bounds__(kMaxThreads) void qk_norm_rope_kernel(RopeArgs a) {
+  prologue_body<IO, W, TB, INTERLEAVED, APPEND, false, kMaxThreads>(a);
+}
+
+// The projection's epilogue: more registers per thread (the partials), so a
+// smaller workgroup bound.
+template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND>
+__global__ __launch_bounds__(kMaxProjThreads) void qkv_epilogue_kernel(RopeArgs a) {
+  prologue_body<IO, W, TB, INTERLEAVED, APPEND, true, kMaxProjThreads>(a);
+}
+
 template <typename IO, typename W, typename TB, bool APPEND>
 hipError_t launch3(const RopeArgs& a, int tokens, int threads, bool interleaved,
                    hipStream_t st) {
+  if (a.part) {
+    if (interleaved)
+      hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, true, APPEND>), dim3(tokens),
+                         dim3(threads), 0, st, a);
+    else
+      hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, false, APPEND>), dim3(tokens),
+                         dim3(threads), 0, st, a);
+    return hipGetLastError();
+  }
   if (interleaved)
     hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, true, APPEND>), dim3(tokens),
                        dim3(threads), 0, st, a);
@@ -414,4 +514,140 @@ extern "C" int dx_qk_norm_rope_append_dev(
                     q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity, 0,
                     static_cast<const int32_t*>(start_dev), static_cast<int32_t*>(status), B, L,
                     H, D, eps, interleaved, stream, true);
+}
+
+// ---------------------------------------------------------------------------
+// Fused QKV projection: split-K GEMM (qkv_gemm.hip), then the prologue kernel
+// reading its partials (sum, bias, one rounding: the projection's output),
+// with the cache write when a cache is given.
+// ---------------------------------------------------------------------------
+static int qkv_entry(const void* x, int64_t x_sb, int64_t x_sl, int io_dtype, const void* wq,
+                     const void* wk, const void* wv, int64_t w_row, const void* bq,
+                     const void* bk, const void* bv, const void* qw, const void* kw, int wdt,
+                     const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl, int tdt,
+                     void* q_out, void* k_out, void* v_out, void* cache, int64_t c_plane,
+                     int64_t c_sb, int64_t c_ss, int64_t c_sh, int64_t capacity, int64_t start,
+                     const int32_t* start_dev, int32_t* status, int64_t B, int64_t L,
+                     int64_t C, int64_t H, int64_t D, float eps, int interleaved,
+                     void* workspace, int64_t ws_bytes, void* stream) {
+  DX_CHECK_ARG(io_dtype == DX_BF16 || io_dtype == DX_F16,
+               "qkv_norm_rope: io dtype must be bf16 or f16 (got code %d)", io_dtype);
+  DX_CHECK_ARG(wdt == DX_BF16 || wdt == DX_F16 || wdt == DX_F32,
+               "qkv_norm_rope: weight dtype code %d unsupported", wdt);
+  DX_CHECK_ARG(tdt == DX_BF16 || tdt == DX_F16 || tdt == DX_F32,
+               "qkv_norm_rope: cos/sin dtype code %d unsupported", tdt);
+  DX_CHECK_ARG(B >= 0 && L >= 0 && H > 0 && D > 0 && C > 0, "qkv_norm_rope: bad shape");
+  const int64_t M = B * L, HD = H * D;
+  DX_CHECK_ARG(M <= 128, "qkv_norm_rope: %lld tokens exceed 128 (decode chunks only)",
+               (long long)M);
+  DX_CHECK_ARG(D % 16 == 0 && HD % 128 == 0 && HD <= int64_t(kMaxProjThreads) * 16,
+               "qkv_norm_rope: H*D = %lld must be a multiple of 128 and at most %d, head_dim "
+               "a multiple of 16", (long long)HD, kMaxProjThreads * 16);
+  DX_CHECK_ARG(C % 512 == 0, "qkv_norm_rope: C = %lld must be a multiple of 512", (long long)C);
+  DX_CHECK_ARG(x && wq && wk && wv && qw && kw && cos && sin && q_out && k_out && v_out,
+               "qkv_norm_rope: null pointer");
+  DX_CHECK_ARG(aligned16(x) && aligned16(wq) && aligned16(wk) && aligned16(wv) &&
+                   aligned16(q_out) && aligned16(k_out) && aligned16(v_out) &&
+                   aligned16(qw) && aligned16(kw) && aligned16(cos) && aligned16(sin) &&
+                   (!bq || aligned16(bq)) && (!bk || aligned16(bk)) && (!bv || aligned16(bv)),
+               "qkv_norm_rope: pointers must be 16-byte aligned");
+  DX_CHECK_ARG(x_sb % 8 == 0 && x_sl % 8 == 0 && w_row % 8 == 0 && w_row >= C,
+               "qkv_norm_rope: strides must be multiples of 8 elements (weight rows >= C)");
+  const int64_t per16 = (tdt == DX_F32) ? 4 : 8;
+  DX_CHECK_ARG(cos_sl % per16 == 0 && sin_sl % per16 == 0,
+               "qkv_norm_rope: cos/sin row strides must keep rows 16-byte aligned");
+  const bool append = cache != nullptr;
+  if (append) {
+    DX_CHECK_ARG(start >= 0, "qkv_norm_rope: negative start");
+    DX_CHECK_ARG(!start_dev || (reinterpret_cast<uintptr_t>(start_dev) & 3u) == 0,
+                 "qkv_norm_rope: device start must be a 4-byte aligned int32");
+    if (!start_dev && start + L > capacity) {
+      set_error("KV cache full: %lld + %lld > %lld", (long long)start, (long long)L,
+                (long long)capacity);
+      return DX_EFULL;
+    }
+    DX_CHECK_ARG(aligned16(cache) && c_plane % 8 == 0 && c_sb % 8 == 0 && c_ss % 8 == 0 &&
+                     c_sh % 8 == 0,
+                 "qkv_norm_rope: cache must be 16-byte aligned with strides that are "
+                 "multiples of 8 elements");
+  }
+  if (M == 0) return DX_OK;
+  const QkvPlan plan = plan_qkv(M, C, HD);
+  if (!workspace || ws_bytes < plan.workspace_bytes) {
+    set_error("qkv_norm_rope: workspace of %lld bytes needed, %lld given",
+              (long long)plan.workspace_bytes, (long long)ws_bytes);
+    return DX_EWORKSPACE;
+  }
+  DX_CHECK_ARG(aligned16(workspace), "qkv_norm_rope: workspace must be 16-byte aligned");
+
+  QkvGemmArgs g{};
+  g.x = static_cast<const uint16_t*>(x); g.x_sb = x_sb; g.x_sl = x_sl;
+  g.w[0] = static_cast<const uint16_t*>(wq);
+  g.w[1] = static_cast<const uint16_t*>(wk);
+  g.w[2] = static_cast<const uint16_t*>(wv);
+  g.w_row[0] = g.w_row[1] = g.w_row[2] = w_row;
+  g.part = static_cast<float*>(workspace);
+  g.M = int(M); g.L = int(L); g.C = int(C); g.HD = int(HD); g.S = plan.splits;
+  g.Kc = int(C / plan.splits);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_qkv_gemm(g, plan, io_dtype, st);
+  if (e != hipSuccess) {
+    set_error("qkv_norm_rope: projection launch failed: %s", hipGetErrorString(e));
+    return DX_ELAUNCH;
+  }
+
+  RopeArgs a{};
+  a.qw = qw; a.kw = kw; a.cos = cos; a.cos_sl = cos_sl; a.sin = sin; a.sin_sl = sin_sl;
+  a.q_out = static_cast<uint16_t*>(q_out); a.k_out = static_cast<uint16_t*>(k_out);
+  a.v_out = static_cast<uint16_t*>(v_out);
+  a.part = g.part; a.part_split = M * 3 * HD; a.n_part = plan.splits;
+  a.bias[0] = static_cast<const uint16_t*>(bq);
+  a.bias[1] = static_cast<const uint16_t*>(bk);
+  a.bias[2] = static_cast<const uint16_t*>(bv);
+  if (append) {
+    a.ck = static_cast<uint16_t*>(cache);
+    a.cv = static_cast<uint16_t*>(cache) + c_plane;
+    a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh; a.start = start;
+    a.start_dev = start_dev; a.status = status; a.capacity = capacity;
+  }
+  a.L = int(L); a.H = int(H); a.D = int(D); a.eps = eps;
+  const int units = int(HD / 16);
+  const int threads = (units + 63) / 64 * 64;
+  if (io_dtype == DX_BF16)
+    e = append ? launch1<bf16_t, true>(a, int(M), threads, wdt, tdt, interleaved != 0, st)
+               : launch1<bf16_t, false>(a, int(M), threads, wdt, tdt, interleaved != 0, st);
+  else
+    e = append ? launch1<f16_t, true>(a, int(M), threads, wdt, tdt, interleaved != 0, st)
+               : launch1<f16_t, false>(a, int(M), threads, wdt, tdt, interleaved != 0, st);
+  if (e != hipSuccess) {
+    set_error("qkv_norm_rope: epilogue launch failed: %s", hipGetErrorString(e));
+    return DX_ELAUNCH;
+  }
+  return DX_OK;
+}
+
+extern "C" int64_t dx_qkv_workspace_bytes(int64_t B, int64_t L, int64_t C, int64_t H,
+                                          int64_t D) {
+  if (B < 0 || L < 0 || C <= 0 || H <= 0 || D <= 0) {
+    set_error("qkv_workspace_bytes: bad shape");
+    return -DX_EINVAL;
+  }
+  if (B * L == 0) return 0;
+  return plan_qkv(B * L, C, H * D).workspace_bytes;
+}
+
+extern "C" int dx_qkv_norm_rope(
+    const void* x, int64_t x_sb, int64_t x_sl, int io_dtype, const void* wq, const void* wk,
+    const void* wv, int64_t w_row, const void* bq, const void* bk, const void* bv,
+    const void* q_weight, const void* k_weight, int weight_dtype, const void* cos,
+    int64_t cos_sl, const void* sin, int64_t sin_sl, int table_dtype, void* q_out, void* k_out,
+    void* v_out, void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+    int64_t capacity, int64_t start, const void* start_dev, void* status, int64_t B,
+    int64_t L, int64_t C, int64_t H, int64_t D, float eps, int interleaved, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  return qkv_entry(x, x_sb, x_sl, io_dtype, wq, wk, wv, w_row, bq, bk, bv, q_weight, k_weight,
+                   weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype, q_out, k_out, v_out,
+                   cache, c_plane, c_sb, c_ss, c_sh, capacity, start,
+                   static_cast<const int32_t*>(start_dev), static_cast<int32_t*>(status), B, L,
+                   C, H, D, eps, interleaved, workspace, workspace_bytes, stream);
 }

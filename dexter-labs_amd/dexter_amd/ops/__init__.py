@@ -10,6 +10,10 @@ and calls it, exactly as dexter's dispatchers do (``python/dexter/ops/__init__.p
 * ``kv_cache_append``            -> ``select("cache", "append", cache, k, v)``
   (no dispatcher in the reference: ``KVCache.append`` does two torch slice
   copies, ``models/dreamzero/model.py:53-58``; here it is a kernel too)
+* ``qkv_norm_rope``              -> ``select("rope", "qkv_norm_rope", x, wq, ...)``
+  (no dispatcher in the reference: ``SelfAttention.forward`` runs three
+  ``nn.Linear`` and ``ops.qk_norm_rope``, ``models/dreamzero/model.py:162-175``;
+  here one call for decode chunks)
 * ``adaln_modulate``             -> ``select("norm", "adaln", x, scale, shift)``
   (reference ``ops/__init__.py:39-49``; same arguments and default eps)
 * ``gated_residual``             -> ``select("norm", "gated_residual", x, y, gate)``
@@ -28,7 +32,35 @@ from ..registry import select
 
 __all__ = ["qk_norm_rope", "blockwise_causal_attention", "kv_cache_append",
            "qk_norm_rope_append", "blockwise_causal_attention_varlen",
-           "adaln_modulate", "gated_residual"]
+           "adaln_modulate", "gated_residual", "qkv_norm_rope"]
+
+
+def qkv_norm_rope(
+    x: torch.Tensor,
+    wq: torch.Tensor, bq: torch.Tensor | None,
+    wk: torch.Tensor, bk: torch.Tensor | None,
+    wv: torch.Tensor, bv: torch.Tensor | None,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    heads: int,
+    eps: float = 1e-6,
+    interleaved: bool = True,
+    cache: torch.Tensor | None = None,
+    start: int | torch.Tensor = 0,
+    status: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The q/k/v projections of a ``[B, L, C]`` chunk, QK-norm + rotary, and the cache write.
+
+    Equals ``q, k, v = F.linear(x, wq, bq), F.linear(x, wk, bk), F.linear(x, wv, bv)``
+    viewed as ``[B, L, heads, D]``, then ``qk_norm_rope(q, k, ...)``, and, with a
+    ``cache``, ``kv_cache_append(cache, k_rotated, v, start, status)``. Returns the
+    rotated ``q``, ``k`` and the projected ``v``.
+    """
+    return select("rope", "qkv_norm_rope", x, wq, bq, wk, bk, wv, bv, q_weight, k_weight, cos,
+                  sin, heads)(x, wq, bq, wk, bk, wv, bv, q_weight, k_weight, cos, sin, heads,
+                              eps, interleaved, cache, start, status)
 
 
 def adaln_modulate(

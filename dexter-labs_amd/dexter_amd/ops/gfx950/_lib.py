@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -109,6 +109,19 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         _f, _i, _p]),
     "dx_attention_workspace_bytes": (_l, [_l, _l, _l, _l, _l, _l,
                                           ctypes.POINTER(ctypes.c_int64)]),
+    "dx_qkv_norm_rope": (_i, [
+        _p, _l, _l, _i,            # x, sb, sl, io dtype
+        _p, _p, _p, _l,            # wq, wk, wv, weight row stride
+        _p, _p, _p,                # bq, bk, bv (may be null)
+        _p, _p, _i,                # q/k norm weights, dtype
+        _p, _l, _p, _l, _i,        # cos, cos_sl, sin, sin_sl, table dtype
+        _p, _p, _p,                # q_out, k_out, v_out
+        _p, _l, _l, _l, _l,        # cache (may be null), plane, sb, ss, sh
+        _l, _l, _p, _p,            # capacity, start, device start, status
+        _l, _l, _l, _l, _l,        # B, L, C, H, D
+        _f, _i,                    # eps, interleaved
+        _p, _l, _p]),              # workspace, bytes, stream
+    "dx_qkv_workspace_bytes": (_l, [_l, _l, _l, _l, _l]),
     "dx_adaln_modulate": (_i, [
         _p, _l, _l, _i,            # x, sb, sl, x dtype
         _p, _l, _l,                # scale, sb, sl

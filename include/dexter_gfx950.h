@@ -25,6 +25,11 @@
  *                            captured graph serves every control step while
  *                            the cache grows; the reference captures only
  *                            cache-free steps (runtime/graph.py:50-74)
+ *   dx_qkv_norm_rope         the q/k/v projections of SelfAttention.forward
+ *                            (models/dreamzero/model.py:162-165, three
+ *                            nn.Linear calls; on gfx1151 hipBLASLt through
+ *                            ops/gfx1151/gemm) fused with dx_qk_norm_rope(_append)
+ *                            (model.py:166-175)
  *   dx_adaln_modulate        ops/gfx1151/norm/adaln.py:108-128 (kernel :20-48;
  *                            semantics ops/reference/norm.py:16-20, dispatcher
  *                            ops/__init__.py:39-49)
@@ -71,7 +76,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 5
+#define DX_ABI_VERSION 6
 
 /*
  * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.
@@ -239,6 +244,40 @@ int dx_qk_norm_rope_append_dev(const void* q, int64_t q_sb, int64_t q_sl, int64_
 int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
                                      int64_t D, int64_t cache_len,
                                      const int64_t* cache_lens);
+
+/*
+ * QKV projection of a decode chunk fused with the QK-RMSNorm + rotary
+ * prologue and the KV-cache write:
+ *   q = x wq^T + bq, k = x wk^T + bk, v = x wv^T + bv   (nn.Linear, rounded
+ *       once to io_dtype: the projections' outputs)
+ *   (q_out, k_out) = dx_qk_norm_rope(q, k, ...), v_out = v
+ *   and, when cache != NULL, the rotated k and v written to rows
+ *   [start, start + L) of the cache (start from start_dev when that is not
+ *   NULL, with the device-cursor rules of dx_kv_append_dev).
+ * x is [B, L, C] (strides x_sb, x_sl; C contiguous); wq/wk/wv are [H*D, C]
+ * (row stride w_row, the nn.Linear weight layout); bq/bk/bv are [H*D] or NULL.
+ * q_out, k_out, v_out are contiguous [B, L, H, D]. Limits: B*L <= 128 tokens
+ * (decode chunks), C a multiple of 512, H*D a multiple of 128 and at most
+ * 8192. workspace: dx_qkv_workspace_bytes(...) bytes, 16-byte aligned (fp32
+ * split-K partial products; no initialisation needed).
+ * Replaces: models/dreamzero/model.py:162-175 (three nn.Linear, then
+ * ops.qk_norm_rope and KVCache.append).
+ */
+int dx_qkv_norm_rope(const void* x, int64_t x_sb, int64_t x_sl, int io_dtype,
+                     const void* wq, const void* wk, const void* wv, int64_t w_row,
+                     const void* bq, const void* bk, const void* bv,
+                     const void* q_weight, const void* k_weight, int weight_dtype,
+                     const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl,
+                     int table_dtype,
+                     void* q_out, void* k_out, void* v_out,
+                     void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                     int64_t capacity, int64_t start, const void* start_dev, void* status,
+                     int64_t B, int64_t L, int64_t C, int64_t H, int64_t D,
+                     float eps, int interleaved,
+                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes dx_qkv_norm_rope needs for this shape; negative DX_E* on a bad shape. */
+int64_t dx_qkv_workspace_bytes(int64_t B, int64_t L, int64_t C, int64_t H, int64_t D);
 
 /*
  * Adaptive LayerNorm modulation of a [B, L, C] activation:

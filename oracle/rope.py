@@ -11,6 +11,10 @@ Follows ``python/dexter/ops/reference/rope.py``:
   ``lo*s + hi*c`` with cos/sin ``[L, D/2]`` broadcast over batch and heads;
   cast to the input dtype -- the second rounding.
 * ``qk_norm_rope`` (:43-56): norm then rotary, for q and k.
+* ``qkv_project`` restates the three ``nn.Linear`` projections in front of it
+  (``models/dreamzero/model.py:162-165``): fp32 products and sums of the io-dtype
+  operands plus the bias, rounded once to the io dtype (what a bf16
+  ``F.linear`` returns, up to the summation order).
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 """
@@ -53,3 +57,17 @@ def qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps: float = 1e-6,
     qn, kn = rms_norm(q, q_weight, eps), rms_norm(k, k_weight, eps)
     return (rotary(qn, cos, sin, interleaved, keep_fp32),
             rotary(kn, cos, sin, interleaved, keep_fp32))
+
+
+def qkv_project(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, heads: int,
+                keep_fp64: bool = False) -> torch.Tensor:
+    """``F.linear(x, w, b)`` of ``x [B, L, C]``, viewed as ``[B, L, heads, D]``.
+
+    Computed in fp64 from the io-dtype operands; rounded once to x's dtype
+    unless ``keep_fp64``.
+    """
+    y = x.double() @ w.double().t()
+    if b is not None:
+        y = y + b.double()
+    y = y.reshape(x.shape[0], x.shape[1], heads, -1)
+    return y if keep_fp64 else y.to(x.dtype)

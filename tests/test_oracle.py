@@ -308,6 +308,21 @@ def test_pairings_differ():
     assert not torch.allclose(a.float(), b.float(), atol=1e-3)
 
 
+def test_qkv_project_is_linear():
+    """The projection restatement against torch's F.linear (fp32) and a closed form."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 5, 64, generator=g).to(torch.bfloat16)
+    w = (torch.randn(48, 64, generator=g) * 0.1).to(torch.bfloat16)
+    b = torch.randn(48, generator=g).to(torch.bfloat16)
+    got = orope.qkv_project(x, w, b, heads=3, keep_fp64=True)
+    lib = F.linear(x.float(), w.float(), b.float()).reshape(2, 5, 3, 16)
+    torch.testing.assert_close(got.float(), lib, rtol=1e-5, atol=1e-5)
+    eye = torch.eye(64, dtype=torch.bfloat16)
+    same = orope.qkv_project(x, eye, None, heads=4)
+    assert torch.equal(same.reshape(2, 5, 64), x)
+    assert orope.qkv_project(x, w, b, heads=3).dtype == torch.bfloat16
+
+
 # ------------------------------------------------------------ kv cache -----
 
 def test_kv_cache_contract():

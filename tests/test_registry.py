@@ -72,6 +72,7 @@ def test_gates_do_not_cross():
     ("cache/append", "hip_kv_append_gfx950"),
     ("rope/qk_norm_rope_append", "hip_qk_norm_rope_append_gfx950"),
     ("attention/blockwise_causal_varlen", "hip_blockwise_causal_varlen_gfx950"),
+    ("rope/qkv_norm_rope", "hip_qkv_norm_rope_gfx950"),
     ("norm/adaln", "hip_adaln_gfx950"),
     ("norm/gated_residual", "hip_gated_residual_gfx950"),
 ])
