@@ -146,3 +146,30 @@ def test_rejects_long_chunks(device, built_lib):
     x, ws, bs, nq, nk, cos, sin = _setup(1, 129, 512, 2, 64)
     with pytest.raises(LookupError):
         ops.qkv_norm_rope(x, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], nq, nk, cos, sin, 2)
+
+
+@pytest.mark.parametrize("write", [False, True])
+def test_self_attention_fused_projection_matches_unfused(device, built_lib, write):
+    """SelfAttention over a decode chunk with and without the fused projection."""
+    from dexter_amd.models import KVCache, SelfAttention
+    torch.manual_seed(3)
+    dim, heads, rows = 1024, 8, 83
+    layer = SelfAttention(dim, heads, dtype=DT, device=device)
+    with torch.no_grad():
+        for lin in (layer.q, layer.k, layer.v, layer.o):
+            lin.weight.normal_(0, dim ** -0.5)
+        layer.q_norm.copy_(1 + 0.1 * torch.randn(dim))
+        layer.k_norm.copy_(1 + 0.1 * torch.randn(dim))
+    cos, sin = (t.to(device) for t in rope_table(torch.arange(rows) + 83, dim // heads))
+    caches = [KVCache(1, 1, 300, heads, dim // heads, device, DT) for _ in range(2)]
+    hist = _setup(1, 83, dim, heads, dim // heads, seed=21)[0]
+    for c in caches:  # the same history through the unfused path
+        layer(hist, cos, sin, c, 0, write=True, fused_qkv=False)
+        c.commit(rows)
+    x = torch.randn(1, rows, dim, device=device).to(DT)
+    fused = layer(x, cos, sin, caches[0], 0, write=write, fused_qkv=True)
+    plain = layer(x, cos, sin, caches[1], 0, write=write, fused_qkv=False)
+    assert_parity_scaled(fused, plain.float(), what=f"write={write}")
+    if write:
+        assert_parity_scaled(caches[0].cache[0][:, :, 83:166], caches[1].cache[0][:, :, 83:166].float(),
+                             what="appended rows")
