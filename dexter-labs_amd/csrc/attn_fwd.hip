@@ -557,15 +557,20 @@ struct Coord {
 // group g share XCD g % 8.
 __device__ __forceinline__ void split_index(int i, int G, bool contiguous, int& gidx,
                                             int& rank) {
-  if ((G & 7) == 0) {
-    const int xcd = i & 7, slot = i >> 3, g8 = G >> 3;
+  // Unsigned arithmetic throughout: every index is non-negative, and unsigned
+  // division by a uniform value is shorter than signed.
+  const uint32_t ui = uint32_t(i), uG = uint32_t(G);
+  if ((uG & 7u) == 0) {
+    const uint32_t xcd = ui & 7u, slot = ui >> 3, g8 = uG >> 3;
+    const uint32_t q = slot / g8, rem = slot - q * g8;
     // contiguous: XCD x takes groups [x G/8, (x+1) G/8), so heads that share
     // a K/V head (adjacent under grouped-query attention) share an L2.
-    gidx = contiguous ? xcd * g8 + slot % g8 : xcd + 8 * (slot % g8);
-    rank = slot / g8;
+    gidx = int(contiguous ? xcd * g8 + rem : xcd + 8u * rem);
+    rank = int(q);
   } else {
-    gidx = i % G;
-    rank = i / G;
+    const uint32_t q = ui / uG;
+    gidx = int(ui - q * uG);
+    rank = int(q);
   }
 }
 
@@ -592,14 +597,16 @@ __device__ __forceinline__ Coord locate(const AttnArgs& a, int idx, bool combine
     seg_item_base = a.seg_base[s];
     c.b = a.seg_b[s];
   }
-  const int per_q = combine ? chunks : c.n_splits;
+  const uint32_t per_q = uint32_t(combine ? chunks : c.n_splits);
   int gidx, rank;
   split_index(local, G, a.kv_group > 1, gidx, rank);
-  c.split = rank % per_q;
-  c.qtile = a.n_qtiles - 1 - rank / per_q;  // heaviest (latest) query tiles first
+  const uint32_t rq = uint32_t(rank) / per_q;
+  c.split = int(uint32_t(rank) - rq * per_q);
+  c.qtile = a.n_qtiles - 1 - int(rq);  // heaviest (latest) query tiles first
   if (a.n_seg == 0) {
-    c.b = gidx / a.H;
-    c.h = gidx % a.H;
+    const uint32_t bq = uint32_t(gidx) / uint32_t(a.H);
+    c.b = int(bq);
+    c.h = gidx - int(bq) * a.H;
   } else {
     c.h = gidx;
   }
@@ -946,8 +953,10 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 
   const int n_ct = (cache_len + kBN - 1) / kBN;
   const int n_tiles = n_ct + (kv_max - cache_len + kBN - 1) / kBN;
-  const int t_begin = int((int64_t(it.split) * n_tiles) / it.n_splits);
-  const int t_end = int((int64_t(it.split + 1) * n_tiles) / it.n_splits);
+  // 32-bit unsigned: splits <= 16 and tiles < 2^26 (keys < 2^30), so the
+  // products fit, and the division is far shorter than a 64-bit one.
+  const int t_begin = int(uint32_t(it.split) * uint32_t(n_tiles) / uint32_t(it.n_splits));
+  const int t_end = int(uint32_t(it.split + 1) * uint32_t(n_tiles) / uint32_t(it.n_splits));
   const int iters = (t_end - t_begin + NS - 1) / NS;  // barrier rounds, equal for all streams
 
   KvSrc src;
@@ -1351,8 +1360,10 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   const int kv_max = cache_len + visible_end(a, min(q0 + BM, a.Lq) - 1);
   const int n_ct = (cache_len + kBN - 1) / kBN;
   const int n_tiles = n_ct + (kv_max - cache_len + kBN - 1) / kBN;
-  const int t_begin = int((int64_t(it.split) * n_tiles) / it.n_splits);
-  const int t_end = int((int64_t(it.split + 1) * n_tiles) / it.n_splits);
+  // 32-bit unsigned: splits <= 16 and tiles < 2^26 (keys < 2^30), so the
+  // products fit, and the division is far shorter than a 64-bit one.
+  const int t_begin = int(uint32_t(it.split) * uint32_t(n_tiles) / uint32_t(it.n_splits));
+  const int t_end = int(uint32_t(it.split + 1) * uint32_t(n_tiles) / uint32_t(it.n_splits));
   const int nt = t_end - t_begin;
 
   KvSrc src;
