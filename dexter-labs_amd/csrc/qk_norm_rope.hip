@@ -10,14 +10,15 @@
 // Keeping the reference's intermediate rounding makes this kernel agree with
 // the oracle to within the summation order of the mean.
 //
-// Work layout: one workgroup per (batch, token), one thread per "unit" of 8
-// rotary pairs: 16 consecutive elements when pairs are interleaved
-// (2j, 2j+1), or 8 elements at offset o plus 8 at o + D/2 for split-half
-// pairs. The workgroup is the unit count rounded up to whole waves (192
-// threads for a 3072-wide plane). The kernel is latency-bound at decode
-// sizes, so every global load a thread needs -- q, k, both weights, cos, sin
-// (and v for the cache write) -- is issued before the sum-of-squares
-// reduction: one memory round trip, then LDS, then the stores.
+// Work layout: one workgroup per (batch, token) for q and k together, or, when
+// v is written too (cache append, projection partials), one per (batch, token)
+// and plane; one thread per "unit" of 8 rotary pairs: 16 consecutive elements when pairs are
+// interleaved (2j, 2j+1), or 8 elements at offset o plus 8 at o + D/2 for
+// split-half pairs. The workgroup is the unit count rounded up to whole waves
+// (192 threads for a 3072-wide plane). The kernel is latency-bound at decode
+// sizes, so every global load a thread needs -- its rows, weights, cos and
+// sin -- is issued before the sum-of-squares reduction: one memory round
+// trip, then LDS, then the stores.
 #include "dx_common.h"
 #include "qkv_gemm.h"
 
@@ -106,6 +107,9 @@ struct RopeArgs {
   const uint16_t* bias[3];                // q, k, v bias rows [H D], each may be null
   uint16_t* v_out;
   int n_part;
+  // floor(u / (D / 16)) = (u * uph_magic) >> 21 for every thread index u < 1024
+  // (uph_magic = 2^21 / (D / 16) + 1; checked exhaustively for D / 16 <= 1024).
+  uint32_t uph_magic;
 };
 
 // Touch every 64-byte line of the arguments up front: independent scalar
@@ -121,203 +125,233 @@ __device__ __forceinline__ void prefetch_args(const RopeArgs& a) {
   asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3), "s"(l4));
 }
 
-// The projection's output for this thread's six 8-element pieces (q, k, v at
-// the lo and hi offsets): the sum of the split-K partials in split order, plus
-// the bias, rounded to IO once. Partials are read two at a time with all
-// twelve loads of a partial issued together, so the pieces share round trips.
+// The projection's output for this thread's two 8-element pieces of one plane
+// (the lo and hi offsets of ``row``): the sum of the split-K partials in split
+// order, plus the bias (may be null), rounded to IO once. Partials are read
+// four at a time, all their loads issued together, so they share round trips.
 template <typename IO>
-__device__ __forceinline__ void projected(const RopeArgs& a, const float* row, int64_t hd,
-                                          int lo, int hi, int64_t boff, u32x4 (&q)[2],
-                                          u32x4 (&k)[2], u32x4 (&v)[2]) {
-  const int64_t off[6] = {lo, hi, hd + lo, hd + hi, 2 * hd + lo, 2 * hd + hi};
-  f32x4 s[6][2];
+__device__ __forceinline__ void projected(const RopeArgs& a, const float* row, int lo, int hi,
+                                          const uint16_t* bias, u32x4 (&x)[2]) {
+  const int off[2] = {lo, hi};
+  f32x4 s[2][2];
 #pragma unroll
-  for (int i = 0; i < 6; ++i) {
+  for (int i = 0; i < 2; ++i) {
     s[i][0] = *reinterpret_cast<const f32x4*>(row + off[i]);
     s[i][1] = *reinterpret_cast<const f32x4*>(row + off[i] + 4);
   }
-  for (int p = 1; p < a.n_part; p += 2) {
-    const float* r1 = row + p * a.part_split;
-    const float* r2 = row + min(p + 1, a.n_part - 1) * a.part_split;
-    const bool two = p + 1 < a.n_part;
-    f32x4 t1[6][2], t2[6][2];
+  for (int p = 1; p < a.n_part; p += 4) {
+    f32x4 t[4][2][2];
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      t1[i][0] = *reinterpret_cast<const f32x4*>(r1 + off[i]);
-      t1[i][1] = *reinterpret_cast<const f32x4*>(r1 + off[i] + 4);
-      t2[i][0] = *reinterpret_cast<const f32x4*>(r2 + off[i]);
-      t2[i][1] = *reinterpret_cast<const f32x4*>(r2 + off[i] + 4);
+    for (int j = 0; j < 4; ++j) {
+      const float* r = row + min(p + j, a.n_part - 1) * a.part_split;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        t[j][i][0] = *reinterpret_cast<const f32x4*>(r + off[i]);
+        t[j][i][1] = *reinterpret_cast<const f32x4*>(r + off[i] + 4);
+      }
     }
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      s[i][0] += t1[i][0];
-      s[i][1] += t1[i][1];
-      if (two) {
-        s[i][0] += t2[i][0];
-        s[i][1] += t2[i][1];
+    for (int j = 0; j < 4; ++j) {
+      if (p + j < a.n_part) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          s[i][0] += t[j][i][0];
+          s[i][1] += t[j][i][1];
+        }
       }
     }
   }
-  u32x4* out[6] = {&q[0], &q[1], &k[0], &k[1], &v[0], &v[1]};
 #pragma unroll
-  for (int i = 0; i < 6; ++i) {
+  for (int i = 0; i < 2; ++i) {
     float f[8] = {s[i][0][0], s[i][0][1], s[i][0][2], s[i][0][3],
                   s[i][1][0], s[i][1][1], s[i][1][2], s[i][1][3]};
-    const uint16_t* b = a.bias[i / 2];
-    if (b) {
+    if (bias) {
       float bf[8];
-      unpack16<IO>(*reinterpret_cast<const u32x4*>(b + boff + (i & 1 ? hi : lo)), bf);
+      unpack16<IO>(*reinterpret_cast<const u32x4*>(bias + off[i]), bf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] += bf[e];
     }
-    u32x4 r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r[j] = pack2<IO>(f[2 * j], f[2 * j + 1]);
-    *out[i] = r;
+    for (int j = 0; j < 4; ++j) x[i][j] = pack2<IO>(f[2 * j], f[2 * j + 1]);
   }
 }
+
+// Cache slot of this call: the host start, or the device start row when one is
+// given (then a block that would not fit is skipped and flagged in *status).
+__device__ __forceinline__ bool cache_start(const RopeArgs& a, bool flag, int64_t& start) {
+  start = a.start;
+  if (!a.start_dev) return true;
+  start = *a.start_dev;
+  const bool fits = start >= 0 && start + a.L <= a.capacity;
+  if (!fits && flag && a.status) a.status[0] = 1;
+  return fits;
+}
+
+// Workgroups per token. When v is written (the cache append, the projection
+// epilogue) q, k and v get one workgroup each (y = 0, 1, 2): three times the
+// workgroups in flight for a latency-bound call, measured faster than one
+// workgroup for all three. The plain q/k form keeps q and k in one workgroup,
+// measured faster than two: their loads share a round trip and one reduction.
+// The q and k planes are normalised over their own H*D elements and rotated;
+// v is copied (or, from partials, summed and rounded) to its outputs.
+template <bool SPLIT> struct Planes {
+  static constexpr int kNorm = SPLIT ? 1 : 2;  // q/k planes per workgroup
+  __device__ static int first(int y) { return SPLIT ? y : 0; }
+  __device__ static bool is_v(int y) { return SPLIT && y == 2; }
+};
 
 template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND, bool PROJ,
           int kThreads>
 __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
+  using PL = Planes<APPEND || PROJ>;
+  constexpr int NP = PL::kNorm;
   prefetch_args(a);
-  __shared__ float red[2][kThreads / 64];
-  const int token = blockIdx.x;  // b * L + l
-  const int b = token / a.L, l = token % a.L;
+  __shared__ float red[NP][kThreads / 64];
+  // Grid (L, planes, B): no division to find the token.
+  const int l = blockIdx.x, y = blockIdx.y, b = blockIdx.z;
+  const int token = b * a.L + l;
+  const bool vplane = PL::is_v(y);  // uniform
+  const int p0 = PL::first(y);      // first q/k plane of this workgroup (0 q, 1 k)
   const int units_per_head = a.D / 16;
   const int n_units = a.H * units_per_head;
   const int u = threadIdx.x;
   const bool active = u < n_units;
-  const int h = active ? u / units_per_head : 0;
-  const int uh = active ? u % units_per_head : 0;
+  // Threads past the last unit (the workgroup is whole waves) load the last
+  // unit's data, add nothing to the sums and store nothing: no branch around
+  // the loads.
+  const int uc = min(u, n_units - 1);
+  const int h = int((uint32_t(uc) * a.uph_magic) >> 21);
+  const int uh = uc - h * units_per_head;
   // Element offsets (within one head) of the lo and hi halves of this unit.
   const int lo = INTERLEAVED ? uh * 16 : uh * 8;
   const int hi = INTERLEAVED ? lo + 8 : lo + a.D / 2;
   const int j0 = INTERLEAVED ? uh * 8 : lo;  // first rotary pair index
+  const int64_t hd = int64_t(a.H) * a.D;
+  const int64_t obase = (int64_t(token) * a.H + h) * a.D;
 
   // ---- every load up front ------------------------------------------------
-  u32x4 qa[2] = {}, ka[2] = {}, va[2] = {};
-  typename Vec8<W>::raw wq[2] = {}, wk[2] = {};
-  typename Vec8<TB>::raw cr = {}, sr = {};
-  if (active && PROJ) {
-    const int64_t hd = int64_t(a.H) * a.D;
-    const float* row = a.part + int64_t(token) * 3 * hd + h * a.D;
-    projected<IO>(a, row, hd, lo, hi, h * a.D, qa, ka, va);
-  }
-  if (active) {
-    if (!PROJ) {
-      const uint16_t* qp = a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh;
-      const uint16_t* kp = a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh;
-      qa[0] = *reinterpret_cast<const u32x4*>(qp + lo);
-      qa[1] = *reinterpret_cast<const u32x4*>(qp + hi);
-      ka[0] = *reinterpret_cast<const u32x4*>(kp + lo);
-      ka[1] = *reinterpret_cast<const u32x4*>(kp + hi);
+  // xa[i]: plane p0 + i (or v); its lo and hi pieces.
+  u32x4 xa[NP][2];
+  typename Vec8<W>::raw wr[NP][2];
+  typename Vec8<TB>::raw cr, sr;
+  {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int plane = vplane ? 2 : p0 + i;
+      if (vplane && i > 0) break;
+      if (PROJ) {
+        const float* row = a.part + int64_t(token) * 3 * hd + plane * hd + h * a.D;
+        const uint16_t* bias = a.bias[plane] ? a.bias[plane] + h * a.D : nullptr;
+        projected<IO>(a, row, lo, hi, bias, xa[i]);
+      } else {
+        const uint16_t* xp =
+            plane == 0 ? a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh
+            : plane == 1 ? a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh
+                         : a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
+        xa[i][0] = *reinterpret_cast<const u32x4*>(xp + lo);
+        xa[i][1] = *reinterpret_cast<const u32x4*>(xp + hi);
+      }
+      if (!vplane) {
+        const W* wp = static_cast<const W*>(plane == 0 ? a.qw : a.kw) + h * a.D;
+        wr[i][0] = Vec8<W>::load(wp + lo);
+        wr[i][1] = Vec8<W>::load(wp + hi);
+      }
     }
-    wq[0] = Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + lo);
-    wq[1] = Vec8<W>::load(static_cast<const W*>(a.qw) + h * a.D + hi);
-    wk[0] = Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + lo);
-    wk[1] = Vec8<W>::load(static_cast<const W*>(a.kw) + h * a.D + hi);
-    cr = Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0);
-    sr = Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0);
-    if (APPEND && !PROJ) {
-      const uint16_t* vp = a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
-      va[0] = *reinterpret_cast<const u32x4*>(vp + lo);
-      va[1] = *reinterpret_cast<const u32x4*>(vp + hi);
+    if (!vplane) {
+      cr = Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0);
+      sr = Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0);
     }
   }
 
-  // ---- sum of squares over the plane ------------------------------------
-  float xq[2][8], xk[2][8];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    unpack16<IO>(qa[p], xq[p]);
-    unpack16<IO>(ka[p], xk[p]);
-  }
-  float sq = 0.f, sk = 0.f;
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sq += xq[p][e] * xq[p][e];
-      sk += xk[p][e] * xk[p][e];
+  if (vplane) {
+    // ---- v: the projection's output and / or the cache row ----------------
+    if (!active) return;
+    if (PROJ) {
+      *reinterpret_cast<u32x4*>(a.v_out + obase + lo) = xa[0][0];
+      *reinterpret_cast<u32x4*>(a.v_out + obase + hi) = xa[0][1];
     }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    sq += __shfl_xor(sq, off, 64);
-    sk += __shfl_xor(sk, off, 64);
+    if (APPEND) {
+      int64_t start;
+      if (cache_start(a, false, start)) {
+        const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
+        *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = xa[0][0];
+        *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = xa[0][1];
+      }
+    }
+    return;
   }
+
+  // ---- sum of squares over each plane -----------------------------------
+  float x[NP][2][8];
+  float sq[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) unpack16<IO>(xa[i][p], x[i][p]);
+    sq[i] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq[i] += x[i][p][e] * x[i][p][e];
+    sq[i] = active ? sq[i] : 0.f;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int i = 0; i < NP; ++i) sq[i] += __shfl_xor(sq[i], off, 64);
   const int wave = threadIdx.x >> 6, n_waves = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0) { red[0][wave] = sq; red[1][wave] = sk; }
+  if ((threadIdx.x & 63) == 0)
+#pragma unroll
+    for (int i = 0; i < NP; ++i) red[i][wave] = sq[i];
   __syncthreads();
   if (!active) return;
-  float tq = 0.f, tk = 0.f;
-  for (int w = 0; w < n_waves; ++w) { tq += red[0][w]; tk += red[1][w]; }
-  const float HD = float(a.H * a.D);
-  const float rq = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tq, HD) + a.eps));
-  const float rk = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(tk, HD) + a.eps));
-
-  // ---- norm (rounded to io, as _rms does), then rotation ------------------
-  float fwq[2][8], fwk[2][8], c[8], s[8];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    Vec8<W>::unpack(wq[p], fwq[p]);
-    Vec8<W>::unpack(wk[p], fwk[p]);
-  }
+  float c[8], s[8];
   Vec8<TB>::unpack(cr, c);
   Vec8<TB>::unpack(sr, s);
+  const float HD = float(hd);
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+  for (int i = 0; i < NP; ++i) {
+    const int plane = p0 + i;
+    float t = 0.f;
+    for (int w = 0; w < n_waves; ++w) t += red[i][w];
+    const float rr = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(t, HD) + a.eps));
+
+    // ---- norm (rounded to io, as _rms does), then rotation ----------------
+    float fw[2][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      xq[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xq[p][e], rq), fwq[p][e]));
-      xk[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(xk[p][e], rk), fwk[p][e]));
+    for (int p = 0; p < 2; ++p) Vec8<W>::unpack(wr[i][p], fw[p]);
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[i][p][e] = round_io<IO>(__fmul_rn(__fmul_rn(x[i][p][e], rr), fw[p][e]));
+    float o[2][8];
+#pragma unroll
+    for (int t8 = 0; t8 < 8; ++t8) {
+      // Interleaved: pair t8 is elements (2 t8, 2 t8 + 1) of the 16-element
+      // span, i.e. half t8 / 4, elements 2 (t8 % 4) and 2 (t8 % 4) + 1.
+      // Split-half: element t8 of half 0 against element t8 of half 1.
+      const int p_lo = INTERLEAVED ? t8 / 4 : 0, e_lo = INTERLEAVED ? 2 * (t8 % 4) : t8;
+      const int p_hi = INTERLEAVED ? t8 / 4 : 1, e_hi = INTERLEAVED ? 2 * (t8 % 4) + 1 : t8;
+      const float xl = x[i][p_lo][e_lo], xh = x[i][p_hi][e_hi];
+      o[p_lo][e_lo] = __fsub_rn(__fmul_rn(xl, c[t8]), __fmul_rn(xh, s[t8]));
+      o[p_hi][e_hi] = __fadd_rn(__fmul_rn(xl, s[t8]), __fmul_rn(xh, c[t8]));
     }
-  float oq[2][8], ok[2][8];
+    u32x4 po[2];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    // Interleaved: pair t is elements (2t, 2t+1) of the 16-element span, i.e.
-    // half t/4, elements 2(t%4) and 2(t%4)+1. Split-half: element t of half 0
-    // against element t of half 1.
-    const int p_lo = INTERLEAVED ? t / 4 : 0, e_lo = INTERLEAVED ? 2 * (t % 4) : t;
-    const int p_hi = INTERLEAVED ? t / 4 : 1, e_hi = INTERLEAVED ? 2 * (t % 4) + 1 : t;
-    const float ql = xq[p_lo][e_lo], qh = xq[p_hi][e_hi];
-    const float kl = xk[p_lo][e_lo], kh = xk[p_hi][e_hi];
-    oq[p_lo][e_lo] = __fsub_rn(__fmul_rn(ql, c[t]), __fmul_rn(qh, s[t]));
-    oq[p_hi][e_hi] = __fadd_rn(__fmul_rn(ql, s[t]), __fmul_rn(qh, c[t]));
-    ok[p_lo][e_lo] = __fsub_rn(__fmul_rn(kl, c[t]), __fmul_rn(kh, s[t]));
-    ok[p_hi][e_hi] = __fadd_rn(__fmul_rn(kl, s[t]), __fmul_rn(kh, c[t]));
-  }
-  u32x4 pq[2], pk[2];
+    for (int p = 0; p < 2; ++p)
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pq[p][j] = pack2<IO>(oq[p][2 * j], oq[p][2 * j + 1]);
-      pk[p][j] = pack2<IO>(ok[p][2 * j], ok[p][2 * j + 1]);
-    }
-  const int64_t obase = (int64_t(token) * a.H + h) * a.D;
-  *reinterpret_cast<u32x4*>(a.q_out + obase + lo) = pq[0];
-  *reinterpret_cast<u32x4*>(a.q_out + obase + hi) = pq[1];
-  *reinterpret_cast<u32x4*>(a.k_out + obase + lo) = pk[0];
-  *reinterpret_cast<u32x4*>(a.k_out + obase + hi) = pk[1];
-  if (PROJ) {
-    *reinterpret_cast<u32x4*>(a.v_out + obase + lo) = va[0];
-    *reinterpret_cast<u32x4*>(a.v_out + obase + hi) = va[1];
-  }
-  if (APPEND) {
-    int64_t start = a.start;
-    bool fits = true;
-    if (a.start_dev) {
-      start = *a.start_dev;
-      fits = start >= 0 && start + a.L <= a.capacity;
-      if (!fits && a.status && token == 0 && u == 0) a.status[0] = 1;
-    }
-    if (fits) {
-      const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
-      *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = pk[0];
-      *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = pk[1];
-      *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = va[0];
-      *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = va[1];
+      for (int j = 0; j < 4; ++j) po[p][j] = pack2<IO>(o[p][2 * j], o[p][2 * j + 1]);
+    uint16_t* out = plane == 0 ? a.q_out : a.k_out;
+    *reinterpret_cast<u32x4*>(out + obase + lo) = po[0];
+    *reinterpret_cast<u32x4*>(out + obase + hi) = po[1];
+    if (APPEND && plane == 1) {
+      int64_t start;
+      if (cache_start(a, token == 0 && u == 0, start)) {
+        const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
+        *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = po[0];
+        *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = po[1];
+      }
     }
   }
 }
@@ -337,21 +371,24 @@ __global__ __launch_bounds__(kMaxProjThreads) void qkv_epilogue_kernel(RopeArgs 
 template <typename IO, typename W, typename TB, bool APPEND>
 hipError_t launch3(const RopeArgs& a, int tokens, int threads, bool interleaved,
                    hipStream_t st) {
+  // Workgroups per token: q, k and v apart when v is written; else q and k
+  // together.
+  const dim3 grid(unsigned(a.L), (APPEND || a.part) ? 3u : 1u, unsigned(tokens / a.L));
   if (a.part) {
     if (interleaved)
-      hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, true, APPEND>), dim3(tokens),
-                         dim3(threads), 0, st, a);
+      hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, true, APPEND>), grid, dim3(threads),
+                         0, st, a);
     else
-      hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, false, APPEND>), dim3(tokens),
-                         dim3(threads), 0, st, a);
+      hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, false, APPEND>), grid, dim3(threads),
+                         0, st, a);
     return hipGetLastError();
   }
   if (interleaved)
-    hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, true, APPEND>), dim3(tokens),
-                       dim3(threads), 0, st, a);
+    hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, true, APPEND>), grid, dim3(threads), 0,
+                       st, a);
   else
-    hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, false, APPEND>), dim3(tokens),
-                       dim3(threads), 0, st, a);
+    hipLaunchKernelGGL((qk_norm_rope_kernel<IO, W, TB, false, APPEND>), grid, dim3(threads), 0,
+                       st, a);
   return hipGetLastError();
 }
 
@@ -393,7 +430,8 @@ int check_common(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
                (long long)D);
   DX_CHECK_ARG(H * D <= int64_t(kMaxThreads) * 16, "qk_norm_rope: H*D = %lld exceeds %d",
                (long long)(H * D), kMaxThreads * 16);
-  DX_CHECK_ARG(B * L < (int64_t(1) << 31), "qk_norm_rope: too many tokens");
+  DX_CHECK_ARG(B * L < (int64_t(1) << 31) && B <= 65535,
+               "qk_norm_rope: too many tokens (B * L < 2^31, B <= 65535)");
   DX_CHECK_ARG(q && k && qw && kw && cos && sin && q_out && k_out,
                "qk_norm_rope: null pointer");
   DX_CHECK_ARG(aligned16(q) && aligned16(k) && aligned16(qw) && aligned16(kw) &&
@@ -455,6 +493,7 @@ static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
     a.start_dev = start_dev; a.status = status; a.capacity = capacity;
   }
   a.L = int(L); a.H = int(H); a.D = int(D); a.eps = eps;
+  a.uph_magic = uint32_t((1u << 21) / uint32_t(D / 16) + 1u);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int tokens = int(B * L);
   const int units = int(H * D / 16);
@@ -611,6 +650,7 @@ static int qkv_entry(const void* x, int64_t x_sb, int64_t x_sl, int io_dtype, co
     a.start_dev = start_dev; a.status = status; a.capacity = capacity;
   }
   a.L = int(L); a.H = int(H); a.D = int(D); a.eps = eps;
+  a.uph_magic = uint32_t((1u << 21) / uint32_t(D / 16) + 1u);
   const int units = int(HD / 16);
   const int threads = (units + 63) / 64 * 64;
   if (io_dtype == DX_BF16)
