@@ -619,8 +619,13 @@ static int qkv_entry(const void* x, int64_t x_sb, int64_t x_sl, int io_dtype, co
   }
   DX_CHECK_ARG(aligned16(workspace), "qkv_norm_rope: workspace must be 16-byte aligned");
 
+  // The GEMM reads x through a buffer descriptor whose offsets are 32-bit.
+  const int64_t x_bytes = 2 * ((B - 1) * x_sb + (L - 1) * x_sl + C);
+  DX_CHECK_ARG(x_bytes < (int64_t(1) << 31), "qkv_norm_rope: x spans %lld bytes (< 2^31)",
+               (long long)x_bytes);
   QkvGemmArgs g{};
   g.x = static_cast<const uint16_t*>(x); g.x_sb = x_sb; g.x_sl = x_sl;
+  g.x_bytes = uint32_t(x_bytes);
   g.w[0] = static_cast<const uint16_t*>(wq);
   g.w[1] = static_cast<const uint16_t*>(wk);
   g.w[2] = static_cast<const uint16_t*>(wv);

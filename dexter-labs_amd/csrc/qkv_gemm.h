@@ -9,6 +9,7 @@ namespace dx {
 // plane = n / HD selects the q, k or v weight ([HD][C] rows, nn.Linear layout).
 struct QkvGemmArgs {
   const uint16_t* x; int64_t x_sb, x_sl;  // activation [B][L][C], element strides
+  uint32_t x_bytes;                        // bytes from x to the end of its last row (< 2^31)
   const uint16_t* w[3]; int64_t w_row[3];  // q, k, v weights: row strides in elements
   float* part;                             // [S][M][3 HD] fp32 partial products
   int M, L, C, HD, S, Kc;                  // tokens, L, in features, H*D, splits, C / S
