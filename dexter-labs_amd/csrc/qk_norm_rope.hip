@@ -10,12 +10,12 @@
 // Keeping the reference's intermediate rounding makes this kernel agree with
 // the oracle to within the summation order of the mean.
 //
-// Work layout: one workgroup per (batch, token) for q and k together, or, when
-// v is written too (cache append, projection partials), one per (batch, token)
-// and plane; one thread per "unit" of 8 rotary pairs: 16 consecutive elements when pairs are
-// interleaved (2j, 2j+1), or 8 elements at offset o plus 8 at o + D/2 for
-// split-half pairs. The workgroup is the unit count rounded up to whole waves
-// (192 threads for a 3072-wide plane). The kernel is latency-bound at decode
+// Work layout: one workgroup per (batch, token) and plane (q, k, and v when v
+// is written: cache append, projection partials); one thread per "unit" of 8
+// rotary pairs: 16 consecutive elements when pairs are interleaved (2j, 2j+1),
+// or 8 elements at offset o plus 8 at o + D/2 for split-half pairs. The
+// workgroup is the unit count rounded up to whole waves (192 threads for a
+// 3072-wide plane). The kernel is latency-bound at decode
 // sizes, so every global load a thread needs -- its rows, weights, cos and
 // sin -- is issued before the sum-of-squares reduction: one memory round
 // trip, then LDS, then the stores.
@@ -187,37 +187,27 @@ __device__ __forceinline__ bool cache_start(const RopeArgs& a, bool flag, int64_
   return fits;
 }
 
-// Workgroups per token. When v is written (the cache append, the projection
-// epilogue) q, k and v get one workgroup each (y = 0, 1, 2): three times the
-// workgroups in flight for a latency-bound call, measured faster than one
-// workgroup for all three. The plain q/k form keeps q and k in one workgroup,
-// measured faster than two: their loads share a round trip and one reduction.
-// The q and k planes are normalised over their own H*D elements and rotated;
-// v is copied (or, from partials, summed and rounded) to its outputs.
-template <bool SPLIT> struct Planes {
-  static constexpr int kNorm = SPLIT ? 1 : 2;  // q/k planes per workgroup
-  __device__ static int first(int y) { return SPLIT ? y : 0; }
-  __device__ static bool is_v(int y) { return SPLIT && y == 2; }
-};
-
+// One workgroup per token and plane: y = 0 is q, y = 1 is k, and y = 2 (only
+// with a cache write or a projection input) is v. More workgroups in flight
+// suit a latency-bound call: measured at the Wan-5B chunk, one workgroup per
+// plane beats one per token for q and k (3.26 against 3.70 us) and for q, k
+// and v (3.81 against 4.38 us with the cache write). The q and k planes are
+// normalised over their own H*D elements and rotated; v is copied (or, from
+// partials, summed and rounded) to its outputs.
 template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND, bool PROJ,
           int kThreads>
 __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
-  using PL = Planes<APPEND || PROJ>;
-  constexpr int NP = PL::kNorm;
   prefetch_args(a);
-  __shared__ float red[NP][kThreads / 64];
+  __shared__ float red[kThreads / 64];
   // Grid (L, planes, B): no division to find the token.
-  const int l = blockIdx.x, y = blockIdx.y, b = blockIdx.z;
+  const int l = blockIdx.x, plane = blockIdx.y, b = blockIdx.z;  // plane: uniform
   const int token = b * a.L + l;
-  const bool vplane = PL::is_v(y);  // uniform
-  const int p0 = PL::first(y);      // first q/k plane of this workgroup (0 q, 1 k)
   const int units_per_head = a.D / 16;
   const int n_units = a.H * units_per_head;
   const int u = threadIdx.x;
   const bool active = u < n_units;
   // Threads past the last unit (the workgroup is whole waves) load the last
-  // unit's data, add nothing to the sums and store nothing: no branch around
+  // unit's data, add nothing to the sum and store nothing: no branch around
   // the loads.
   const int uc = min(u, n_units - 1);
   const int h = int((uint32_t(uc) * a.uph_magic) >> 21);
@@ -230,128 +220,102 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
   const int64_t obase = (int64_t(token) * a.H + h) * a.D;
 
   // ---- every load up front ------------------------------------------------
-  // xa[i]: plane p0 + i (or v); its lo and hi pieces.
-  u32x4 xa[NP][2];
-  typename Vec8<W>::raw wr[NP][2];
+  u32x4 xa[2];
+  typename Vec8<W>::raw wr[2];
   typename Vec8<TB>::raw cr, sr;
-  {
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int plane = vplane ? 2 : p0 + i;
-      if (vplane && i > 0) break;
-      if (PROJ) {
-        const float* row = a.part + int64_t(token) * 3 * hd + plane * hd + h * a.D;
-        const uint16_t* bias = a.bias[plane] ? a.bias[plane] + h * a.D : nullptr;
-        projected<IO>(a, row, lo, hi, bias, xa[i]);
-      } else {
-        const uint16_t* xp =
-            plane == 0 ? a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh
-            : plane == 1 ? a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh
-                         : a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
-        xa[i][0] = *reinterpret_cast<const u32x4*>(xp + lo);
-        xa[i][1] = *reinterpret_cast<const u32x4*>(xp + hi);
-      }
-      if (!vplane) {
-        const W* wp = static_cast<const W*>(plane == 0 ? a.qw : a.kw) + h * a.D;
-        wr[i][0] = Vec8<W>::load(wp + lo);
-        wr[i][1] = Vec8<W>::load(wp + hi);
-      }
-    }
-    if (!vplane) {
-      cr = Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0);
-      sr = Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0);
-    }
+  if (PROJ) {
+    const float* row = a.part + int64_t(token) * 3 * hd + plane * hd + h * a.D;
+    const uint16_t* bias = a.bias[plane] ? a.bias[plane] + h * a.D : nullptr;
+    projected<IO>(a, row, lo, hi, bias, xa);
+  } else {
+    const uint16_t* xp = plane == 0   ? a.q + b * a.q_sb + l * a.q_sl + h * a.q_sh
+                         : plane == 1 ? a.k + b * a.k_sb + l * a.k_sl + h * a.k_sh
+                                      : a.v + b * a.v_sb + l * a.v_sl + h * a.v_sh;
+    xa[0] = *reinterpret_cast<const u32x4*>(xp + lo);
+    xa[1] = *reinterpret_cast<const u32x4*>(xp + hi);
+  }
+  if (plane < 2) {
+    const W* wp = static_cast<const W*>(plane == 0 ? a.qw : a.kw) + h * a.D;
+    wr[0] = Vec8<W>::load(wp + lo);
+    wr[1] = Vec8<W>::load(wp + hi);
+    cr = Vec8<TB>::load(static_cast<const TB*>(a.cos) + l * a.cos_sl + j0);
+    sr = Vec8<TB>::load(static_cast<const TB*>(a.sin) + l * a.sin_sl + j0);
   }
 
-  if (vplane) {
+  if (plane == 2) {
     // ---- v: the projection's output and / or the cache row ----------------
     if (!active) return;
     if (PROJ) {
-      *reinterpret_cast<u32x4*>(a.v_out + obase + lo) = xa[0][0];
-      *reinterpret_cast<u32x4*>(a.v_out + obase + hi) = xa[0][1];
+      *reinterpret_cast<u32x4*>(a.v_out + obase + lo) = xa[0];
+      *reinterpret_cast<u32x4*>(a.v_out + obase + hi) = xa[1];
     }
     if (APPEND) {
       int64_t start;
       if (cache_start(a, false, start)) {
         const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
-        *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = xa[0][0];
-        *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = xa[0][1];
+        *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = xa[0];
+        *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = xa[1];
       }
     }
     return;
   }
 
-  // ---- sum of squares over each plane -----------------------------------
-  float x[NP][2][8];
-  float sq[NP];
+  // ---- sum of squares over the plane ------------------------------------
+  float x[2][8];
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
+  for (int p = 0; p < 2; ++p) unpack16<IO>(xa[p], x[p]);
+  float sq = 0.f;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) unpack16<IO>(xa[i][p], x[i][p]);
-    sq[i] = 0.f;
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int e = 0; e < 8; ++e) sq += x[p][e] * x[p][e];
+  sq = active ? sq : 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sq[i] += x[i][p][e] * x[i][p][e];
-    sq[i] = active ? sq[i] : 0.f;
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-    for (int i = 0; i < NP; ++i) sq[i] += __shfl_xor(sq[i], off, 64);
+  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
   const int wave = threadIdx.x >> 6, n_waves = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0)
-#pragma unroll
-    for (int i = 0; i < NP; ++i) red[i][wave] = sq[i];
+  if ((threadIdx.x & 63) == 0) red[wave] = sq;
   __syncthreads();
   if (!active) return;
-  float c[8], s[8];
+  float t = 0.f;
+  for (int w = 0; w < n_waves; ++w) t += red[w];
+  const float rr = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(t, float(hd)) + a.eps));
+
+  // ---- norm (rounded to io, as _rms does), then rotation ------------------
+  float fw[2][8], c[8], s[8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) Vec8<W>::unpack(wr[p], fw[p]);
   Vec8<TB>::unpack(cr, c);
   Vec8<TB>::unpack(sr, s);
-  const float HD = float(hd);
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int plane = p0 + i;
-    float t = 0.f;
-    for (int w = 0; w < n_waves; ++w) t += red[i][w];
-    const float rr = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(t, HD) + a.eps));
-
-    // ---- norm (rounded to io, as _rms does), then rotation ----------------
-    float fw[2][8];
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) Vec8<W>::unpack(wr[i][p], fw[p]);
+    for (int e = 0; e < 8; ++e) x[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(x[p][e], rr), fw[p][e]));
+  float o[2][8];
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+  for (int t8 = 0; t8 < 8; ++t8) {
+    // Interleaved: pair t8 is elements (2 t8, 2 t8 + 1) of the 16-element span,
+    // i.e. half t8 / 4, elements 2 (t8 % 4) and 2 (t8 % 4) + 1. Split-half:
+    // element t8 of half 0 against element t8 of half 1.
+    const int p_lo = INTERLEAVED ? t8 / 4 : 0, e_lo = INTERLEAVED ? 2 * (t8 % 4) : t8;
+    const int p_hi = INTERLEAVED ? t8 / 4 : 1, e_hi = INTERLEAVED ? 2 * (t8 % 4) + 1 : t8;
+    const float xl = x[p_lo][e_lo], xh = x[p_hi][e_hi];
+    o[p_lo][e_lo] = __fsub_rn(__fmul_rn(xl, c[t8]), __fmul_rn(xh, s[t8]));
+    o[p_hi][e_hi] = __fadd_rn(__fmul_rn(xl, s[t8]), __fmul_rn(xh, c[t8]));
+  }
+  u32x4 po[2];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        x[i][p][e] = round_io<IO>(__fmul_rn(__fmul_rn(x[i][p][e], rr), fw[p][e]));
-    float o[2][8];
+  for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int t8 = 0; t8 < 8; ++t8) {
-      // Interleaved: pair t8 is elements (2 t8, 2 t8 + 1) of the 16-element
-      // span, i.e. half t8 / 4, elements 2 (t8 % 4) and 2 (t8 % 4) + 1.
-      // Split-half: element t8 of half 0 against element t8 of half 1.
-      const int p_lo = INTERLEAVED ? t8 / 4 : 0, e_lo = INTERLEAVED ? 2 * (t8 % 4) : t8;
-      const int p_hi = INTERLEAVED ? t8 / 4 : 1, e_hi = INTERLEAVED ? 2 * (t8 % 4) + 1 : t8;
-      const float xl = x[i][p_lo][e_lo], xh = x[i][p_hi][e_hi];
-      o[p_lo][e_lo] = __fsub_rn(__fmul_rn(xl, c[t8]), __fmul_rn(xh, s[t8]));
-      o[p_hi][e_hi] = __fadd_rn(__fmul_rn(xl, s[t8]), __fmul_rn(xh, c[t8]));
-    }
-    u32x4 po[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) po[p][j] = pack2<IO>(o[p][2 * j], o[p][2 * j + 1]);
-    uint16_t* out = plane == 0 ? a.q_out : a.k_out;
-    *reinterpret_cast<u32x4*>(out + obase + lo) = po[0];
-    *reinterpret_cast<u32x4*>(out + obase + hi) = po[1];
-    if (APPEND && plane == 1) {
-      int64_t start;
-      if (cache_start(a, token == 0 && u == 0, start)) {
-        const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
-        *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = po[0];
-        *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = po[1];
-      }
+    for (int j = 0; j < 4; ++j) po[p][j] = pack2<IO>(o[p][2 * j], o[p][2 * j + 1]);
+  uint16_t* out = plane == 0 ? a.q_out : a.k_out;
+  *reinterpret_cast<u32x4*>(out + obase + lo) = po[0];
+  *reinterpret_cast<u32x4*>(out + obase + hi) = po[1];
+  if (APPEND && plane == 1) {
+    int64_t start;
+    if (cache_start(a, token == 0 && u == 0, start)) {
+      const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
+      *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = po[0];
+      *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = po[1];
     }
   }
 }
@@ -371,9 +335,8 @@ __global__ __launch_bounds__(kMaxProjThreads) void qkv_epilogue_kernel(RopeArgs 
 template <typename IO, typename W, typename TB, bool APPEND>
 hipError_t launch3(const RopeArgs& a, int tokens, int threads, bool interleaved,
                    hipStream_t st) {
-  // Workgroups per token: q, k and v apart when v is written; else q and k
-  // together.
-  const dim3 grid(unsigned(a.L), (APPEND || a.part) ? 3u : 1u, unsigned(tokens / a.L));
+  // Workgroups per token: q and k, and v when it is written.
+  const dim3 grid(unsigned(a.L), (APPEND || a.part) ? 3u : 2u, unsigned(tokens / a.L));
   if (a.part) {
     if (interleaved)
       hipLaunchKernelGGL((qkv_epilogue_kernel<IO, W, TB, true, APPEND>), grid, dim3(threads),
