@@ -176,6 +176,29 @@ __device__ __forceinline__ void projected(const RopeArgs& a, const float* row, i
   }
 }
 
+// Sum over the 64 lanes of a wave, the same bits on every lane, by VALU lane
+// exchanges instead of LDS permutes: DPP within each row of 16 lanes (lanes
+// i ^ 1, i ^ 2, then the half-row and row mirrors), then the gfx950 row swaps
+// (lanes i ^ 16, i ^ 32). Every step adds a lane's value to its partner's,
+// and the partner adds the same two values, so all lanes agree.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf,
+                                                        false));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x = dpp_add<0xb1>(x);   // quad_perm [1, 0, 3, 2]: lane i ^ 1
+  x = dpp_add<0x4e>(x);   // quad_perm [2, 3, 0, 1]: lane i ^ 2
+  x = dpp_add<0x141>(x);  // row_half_mirror: lane 7 - i within 8
+  x = dpp_add<0x140>(x);  // row_mirror: lane 15 - i within 16
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
 // Cache slot of this call: the host start, or the device start row when one is
 // given (then a block that would not fit is skipped and flagged in *status).
 __device__ __forceinline__ bool cache_start(const RopeArgs& a, bool flag, int64_t& start) {
@@ -269,9 +292,7 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
   for (int p = 0; p < 2; ++p)
 #pragma unroll
     for (int e = 0; e < 8; ++e) sq += x[p][e] * x[p][e];
-  sq = active ? sq : 0.f;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+  sq = wave_sum(active ? sq : 0.f);
   const int wave = threadIdx.x >> 6, n_waves = blockDim.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = sq;
   __syncthreads();
