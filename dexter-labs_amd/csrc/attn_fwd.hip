@@ -1120,21 +1120,27 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
   if (NS == 2) {
     // Stream 1 hands (mref, l, acc) to the same lane of stream 0 through LDS,
-    // laid out [value][lane] so consecutive lanes hit consecutive banks.
+    // in 16-byte vectors laid out [vector][lane]: consecutive lanes hit
+    // consecutive 16 bytes, and each lane moves 1 + 4 DT vectors instead of
+    // 2 + 16 DT single floats.
     constexpr int LANES = 64 * kNW;
-    float* x = reinterpret_cast<float*>(smem);
+    static_assert((1 + 4 * DT) * LANES * 16 <= 2 * 2 * Lds<D>::stage * 2,
+                  "the hand-off fits in the tile buffers");
+    f32x4* x = reinterpret_cast<f32x4*>(smem);
     __syncthreads();  // all tile reads done: the LDS is free
     if (stream == 1) {
-      x[ltid] = mref;
-      x[LANES + ltid] = sm.l;
+      x[ltid] = f32x4{mref, sm.l, 0.f, 0.f};
 #pragma unroll
       for (int d = 0; d < DT; ++d)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[(2 + d * 16 + r) * LANES + ltid] = acc[d][r];
+        for (int q = 0; q < 4; ++q)
+          x[(1 + 4 * d + q) * LANES + ltid] =
+              f32x4{acc[d][4 * q], acc[d][4 * q + 1], acc[d][4 * q + 2], acc[d][4 * q + 3]};
     }
     __syncthreads();
     if (stream == 1) return;
-    const float m1 = x[ltid], l1 = x[LANES + ltid];
+    const f32x4 h = x[ltid];
+    const float m1 = h[0], l1 = h[1];
     const float mm = fmaxf(mref, m1);
     const float base = mm == -INFINITY ? 0.f : mm;
     const float w0 = fast_exp2(mref - base), w1 = fast_exp2(m1 - base);
@@ -1142,8 +1148,11 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        acc[d][r] = acc[d][r] * w0 + x[(2 + d * 16 + r) * LANES + ltid] * w1;
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = x[(1 + 4 * d + q) * LANES + ltid];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[d][4 * q + e] = acc[d][4 * q + e] * w0 + v[e] * w1;
+      }
     mref = mm;
   }
 
