@@ -59,7 +59,9 @@
 
 #include <algorithm>
 #include <mutex>
+#include <set>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 namespace dx {
@@ -1773,17 +1775,27 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   return p;
 }
 
+// Opt a kernel into `bytes` of dynamic LDS (beyond the 64 KB default window;
+// gfx950 allows 160 KB per workgroup) on the current device, once per kernel
+// and device: each device holds its own copy of the kernel and its attributes.
+hipError_t opt_in_lds(const void* fn, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lk(mu);
+  if (done.count({fn, dev})) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.insert({fn, dev});
+  return e;
+}
+
 template <int D, typename T, int NS>
 hipError_t launch_main(const AttnArgs& a, int64_t items, hipStream_t st) {
-  // The double-buffered tiles exceed the 64 KB default LDS window: opt in
-  // once per instantiation (gfx950 allows 160 KB per workgroup).
-  constexpr int lds = NS * Lds<D>::bytes;
-  static std::once_flag once;
-  static hipError_t attr = hipSuccess;
-  std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<D, T, NS>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  });
+  constexpr int lds = NS * Lds<D>::bytes;  // double-buffered tiles per stream
+  const hipError_t attr =
+      opt_in_lds(reinterpret_cast<const void*>(&attn_fwd_kernel<D, T, NS>), lds);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL((attn_fwd_kernel<D, T, NS>), dim3(unsigned(items)), dim3(64 * kNW * NS),
                      lds, st, a);
@@ -1793,12 +1805,7 @@ hipError_t launch_main(const AttnArgs& a, int64_t items, hipStream_t st) {
 template <int D, typename T>
 hipError_t launch_pair(const AttnArgs& a, int64_t items, hipStream_t st) {
   constexpr int lds = PairLds<D>::bytes;
-  static std::once_flag once;
-  static hipError_t attr = hipSuccess;
-  std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pair_kernel<D, T>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  });
+  const hipError_t attr = opt_in_lds(reinterpret_cast<const void*>(&attn_pair_kernel<D, T>), lds);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL((attn_pair_kernel<D, T>), dim3(unsigned(items)), dim3(64 * kPairWaves),
                      lds, st, a);
