@@ -5,7 +5,8 @@ implementations (``ops/reference/rope.py:43-56``,
 ``ops/gfx1151/rope/qk_norm_rope.py:93-110``):
 ``(q, k, q_weight, k_weight, cos, sin, eps, interleaved=True) -> (q, k)``.
 The norm spans the whole ``H*D`` plane of a token and the weight is ``H*D``
-long (Wan's QK norm runs before the head split). One workgroup per token.
+long (Wan's QK norm runs before the head split). One workgroup per token and
+plane (q, k, and v when the cache append writes it).
 
 ``rope/qk_norm_rope_append`` is the same pass with the rotated k and the raw
 v also written into rows ``[start, start+L)`` of a ``[2, B, S, H, D]`` cache
