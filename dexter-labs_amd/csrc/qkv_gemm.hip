@@ -25,9 +25,10 @@
 //    chunks are double-buffered, 16-byte pieces XOR-swizzled by row.
 //  * Each split writes its fp32 partial tile to part[s][m][n] with
 //    non-temporal stores (the epilogue reads them from other XCDs, so no L2
-//    reuse is lost; measured 0.5 us faster per call than plain stores); the epilogue
-//    kernel (qk_norm_rope.hip) sums the splits in order, adds the bias,
-//    rounds once to the io type and continues with the QK norm and rotary.
+//    reuse is lost; measured 0.5 us faster per call than plain stores). The
+//    epilogue kernel (qk_norm_rope.hip) sums the splits in order, adds the
+//    bias, rounds once to the io type and continues with the QK norm and
+//    rotary.
 #include "qkv_gemm.h"
 
 #include <algorithm>
