@@ -18,7 +18,10 @@
 // 3072-wide plane). The kernel is latency-bound at decode
 // sizes, so every global load a thread needs -- its rows, weights, cos and
 // sin -- is issued before the sum-of-squares reduction: one memory round
-// trip, then LDS, then the stores.
+// trip, then LDS, then the stores. The outputs are read next by other
+// workgroups (on other XCDs) or much later (the cache rows), so they go out
+// as non-temporal stores: no dirty lines left to write back at the end of the
+// kernel, and the next kernel in the stream starts sooner.
 #include "dx_common.h"
 #include "qkv_gemm.h"
 
@@ -269,15 +272,15 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
     // ---- v: the projection's output and / or the cache row ----------------
     if (!active) return;
     if (PROJ) {
-      *reinterpret_cast<u32x4*>(a.v_out + obase + lo) = xa[0];
-      *reinterpret_cast<u32x4*>(a.v_out + obase + hi) = xa[1];
+      __builtin_nontemporal_store(xa[0], reinterpret_cast<u32x4*>(a.v_out + obase + lo));
+      __builtin_nontemporal_store(xa[1], reinterpret_cast<u32x4*>(a.v_out + obase + hi));
     }
     if (APPEND) {
       int64_t start;
       if (cache_start(a, false, start)) {
         const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
-        *reinterpret_cast<u32x4*>(a.cv + cbase + lo) = xa[0];
-        *reinterpret_cast<u32x4*>(a.cv + cbase + hi) = xa[1];
+        __builtin_nontemporal_store(xa[0], reinterpret_cast<u32x4*>(a.cv + cbase + lo));
+        __builtin_nontemporal_store(xa[1], reinterpret_cast<u32x4*>(a.cv + cbase + hi));
       }
     }
     return;
@@ -329,14 +332,14 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) po[p][j] = pack2<IO>(o[p][2 * j], o[p][2 * j + 1]);
   uint16_t* out = plane == 0 ? a.q_out : a.k_out;
-  *reinterpret_cast<u32x4*>(out + obase + lo) = po[0];
-  *reinterpret_cast<u32x4*>(out + obase + hi) = po[1];
+  __builtin_nontemporal_store(po[0], reinterpret_cast<u32x4*>(out + obase + lo));
+  __builtin_nontemporal_store(po[1], reinterpret_cast<u32x4*>(out + obase + hi));
   if (APPEND && plane == 1) {
     int64_t start;
     if (cache_start(a, token == 0 && u == 0, start)) {
       const int64_t cbase = b * a.c_sb + (start + l) * a.c_ss + h * a.c_sh;
-      *reinterpret_cast<u32x4*>(a.ck + cbase + lo) = po[0];
-      *reinterpret_cast<u32x4*>(a.ck + cbase + hi) = po[1];
+      __builtin_nontemporal_store(po[0], reinterpret_cast<u32x4*>(a.ck + cbase + lo));
+      __builtin_nontemporal_store(po[1], reinterpret_cast<u32x4*>(a.ck + cbase + hi));
     }
   }
 }
