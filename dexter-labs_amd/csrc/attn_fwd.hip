@@ -1605,7 +1605,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   u32x2 w2;
   w2[0] = Mfma<T>::pack(acc[0] * inv, acc[1] * inv);
   w2[1] = Mfma<T>::pack(acc[2] * inv, acc[3] * inv);
-  *reinterpret_cast<u32x2*>(op) = w2;
+  __builtin_nontemporal_store(w2, reinterpret_cast<u32x2*>(op));
 }
 
 // ---------------------------------------------------------------------------
