@@ -236,8 +236,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base
                                            kBufWord3);
 }
 
+// K/V tile loads of the decode kernel: each cache row is read once per call,
+// so the loads are marked non-temporal (cache policy bit NT = 2).
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
 }
 
 // One K tile and one V tile of a workgroup's share, staged in registers
