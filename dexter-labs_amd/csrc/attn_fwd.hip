@@ -909,11 +909,11 @@ __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it,
         u32x2 w;
         w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
         w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
-        __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(po + dim));
+        *reinterpret_cast<u32x2*>(po + dim) = w;
       }
     if (g == 0)
-      __builtin_nontemporal_store(f32x2{any ? mref : -INFINITY, l_tot},
-                                  reinterpret_cast<f32x2*>(a.ws_ml + (pidx * bm + row) * 2));
+      *reinterpret_cast<float2*>(a.ws_ml + (pidx * bm + row) * 2) =
+          make_float2(any ? mref : -INFINITY, l_tot);
   }
 }
 
