@@ -55,6 +55,7 @@
 #include "dx_common.h"
 
 #include <float.h>
+#include <limits.h>
 #include <stdlib.h>
 
 #include <algorithm>
@@ -81,8 +82,8 @@ struct AttnArgs {
   const uint16_t* v; int64_t v_sb, v_sl, v_sh;
   const uint16_t* ck; const uint16_t* cv; int64_t c_sb, c_ss, c_sh;
   uint16_t* out; int64_t o_sb, o_sl, o_sh;
-  uint16_t* ws_o;  // [partials][bm][D] f16 normalised partial outputs acc / l
-  float* ws_ml;    // [partials][bm][2] (exponent reference in log2 units, sum l)
+  uint16_t* ws_o;  // [partials][bm][D] f16 partial outputs acc / l scaled by 2^-e
+  float* ws_ml;    // [partials][bm][4] {exponent reference m (log2 units), sum l, scale exponent e, 0}
   const void* starts; int starts_i64; int n_blocks;
   int B, H, Lq, Lk;
   int kv_group;      // query heads per K/V head (grouped-query attention; 1 = one each)
@@ -103,6 +104,10 @@ struct AttnArgs {
   // (cache_len then holds the cache capacity the launch was planned for), so
   // a captured graph follows the cache as it grows between replays.
   const int32_t* cache_len_dev;
+  // Single-launch decode: one arrival counter per work-item group (indexed by
+  // the group's first partial, 32 ints apart), zero before the launch and
+  // returned to zero by the group's last workgroup.
+  int32_t* counters;
   int seg_b[kMaxSeg], seg_splits[kMaxSeg], seg_cache[kMaxSeg];
   int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
 };
@@ -113,7 +118,8 @@ struct AttnArgs {
 // otherwise issue one after another.
 __device__ __forceinline__ void prefetch_args(const AttnArgs& a) {
   static_assert(offsetof(AttnArgs, n_seg) < 256, "argument header spans four lines");
-  static_assert(offsetof(AttnArgs, cache_len_dev) / 64 == 4, "device cache length on line five");
+  static_assert(offsetof(AttnArgs, cache_len_dev) / 64 == 4 && offsetof(AttnArgs, counters) / 64 == 4,
+                "device cache length and counters on line five");
   const uint64_t l0 = reinterpret_cast<uint64_t>(a.q);
   const uint64_t l1 = uint64_t(a.v_sb);
   const uint64_t l2 = uint64_t(a.c_sh);
@@ -160,33 +166,84 @@ template <> struct Mfma<f16_t> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Block start i, read through the constant address space: the list does not
+// change while a kernel runs, and that lets the compiler use scalar loads
+// (counted by lgkmcnt) instead of vector loads, whose waits would also wait
+// for every tile load in flight.
+typedef __attribute__((address_space(4))) const int32_t const_i32;
+typedef __attribute__((address_space(4))) const int64_t const_i64;
 __device__ __forceinline__ int load_start(const AttnArgs& a, int i) {
-  return a.starts_i64 ? int(static_cast<const int64_t*>(a.starts)[i])
-                      : static_cast<const int32_t*>(a.starts)[i];
+  // A generic pointer to device memory is its global address: convert it
+  // through the integer value.
+  const uint64_t p = reinterpret_cast<uint64_t>(a.starts);
+  return a.starts_i64 ? int(((const_i64*)p)[i]) : ((const_i32*)p)[i];
 }
 
-// End (exclusive, in current-key coordinates) of the keys query i may see.
-// Block b spans [start_b, start_{b+1}) (the last one up to Lq), and a query
-// sees the keys up to the end of its own block. With the starts sorted that
-// end is the first start above i (Lq if none); a query before the first
-// start sees no new key. The starts are read 16 at a time, indices clamped
-// to the last one, so each batch is one round of independent scalar loads
-// instead of a chain of dependent ones.
+// Python's slice bound: index x of a length-n axis, negatives counted from the end.
+__device__ __forceinline__ int slice_at(int x, int n) { return x < 0 ? max(x + n, 0) : min(x, n); }
+
+// The block list as the reference reads it: pairs (lo, hi) of consecutive
+// entries of (starts..., Lq), each setting mask[lo:hi, :hi] (rows by Python
+// slicing, current keys [0, min(hi, Lq))). The starts are read 16 (+1) at a
+// time as independent scalar loads, so each batch is one memory round trip
+// instead of a chain of dependent ones; fn(lo, hi) sees every pair in order.
+template <typename Fn>
+__device__ __forceinline__ void for_each_block(const AttnArgs& a, Fn&& fn) {
+  const int nb = a.n_blocks;
+  for (int base = 0; base < nb; base += 16) {
+    int st[17];
+#pragma unroll
+    for (int u = 0; u < 17; ++u) st[u] = base + u < nb ? load_start(a, base + u) : a.Lq;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (base + u < nb) fn(st[u], st[u + 1]);
+  }
+}
+
+// End (exclusive, in current-key coordinates) of the keys query i may see:
+// the union of the block pairs whose row slice holds i, i.e. the largest
+// min(hi, Lq) among them (a negative hi adds nothing), 0 when no pair holds
+// i (such a row sees only the cache). For ascending starts this is the end of
+// i's own block, and rows before the first start see no current key.
 __device__ __forceinline__ int visible_end(const AttnArgs& a, int i) {
   if (a.causal) return i + 1;
   if (a.n_blocks == 0) return a.Lk;
-  const int nb = a.n_blocks;
-  int e = a.Lq, first = 0;
-  for (int base = 0; base < nb; base += 16) {
-    int st[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) st[u] = load_start(a, min(base + u, nb - 1));
-    if (base == 0) first = st[0];
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      if (st[u] > i) e = min(e, st[u]);
-  }
-  return i < first ? 0 : e;
+  int e = 0;
+  for_each_block(a, [&](int lo, int hi) __attribute__((always_inline)) {
+    if (i >= slice_at(lo, a.Lq) && i < slice_at(hi, a.Lq)) e = max(e, min(hi, a.Lq));
+  });
+  return e;
+}
+
+// Visible-end bounds (current-key coordinates) over the rows [q_first,
+// q_last] of a work item: lo <= visible_end(i) <= hi for each of them.
+// Workgroup-uniform scalar work. With causal, no blocks, or block starts that
+// are ascending and non-negative, visible_end is non-decreasing in i and the
+// end rows give exact bounds. Any other list (the reference accepts one) gets
+// the widest bounds, [0, Lq]: every current tile is visited and masked per
+// key, so results stay exact and only the whole-tile skipping is lost.
+struct EndBounds { int lo, hi; };
+__device__ __forceinline__ EndBounds end_bounds(const AttnArgs& a, int q_first, int q_last) {
+  if (a.causal || a.n_blocks == 0)
+    return {__builtin_amdgcn_readfirstlane(visible_end(a, q_first)),
+            __builtin_amdgcn_readfirstlane(visible_end(a, q_last))};
+  bool ascending = true;
+  int prev = 0;
+  int e_first = 0, e_last = 0;
+  for_each_block(a, [&](int lo, int hi) __attribute__((always_inline)) {
+    ascending = ascending && lo >= prev;
+    prev = lo;
+    if (q_first >= slice_at(lo, a.Lq) && q_first < slice_at(hi, a.Lq))
+      e_first = max(e_first, min(hi, a.Lq));
+    if (q_last >= slice_at(lo, a.Lq) && q_last < slice_at(hi, a.Lq))
+      e_last = max(e_last, min(hi, a.Lq));
+  });
+  // Uniform by construction (kernel arguments and workgroup-uniform rows);
+  // readfirstlane lets the compiler keep the buffer descriptors built from
+  // these bounds in scalar registers.
+  return ascending ? EndBounds{__builtin_amdgcn_readfirstlane(e_first),
+                               __builtin_amdgcn_readfirstlane(e_last)}
+                   : EndBounds{0, a.Lq};
 }
 
 // LDS geometry, per stage: a K tile [64 keys][D] and a V tile [64 keys][D],
@@ -873,11 +930,37 @@ __device__ __forceinline__ void tile_step(const uint16_t* Ks, const uint16_t* Vs
   pv_tile<D, T>(Vs, s, acc, lane);
 }
 
+// Split-KV partial of one row: its normalised output o = acc / l is kept as
+// f16 values o 2^-e, where 2^e is above the row's largest |o| (so every
+// stored value is below 1 in magnitude: no f16 overflow for any finite input,
+// 11 significant bits relative to the row's largest element), plus the fp32
+// record {exponent reference m, sum l, e, 0}. The merge re-weights each split
+// by exp2(m_s - max m) l_s and restores 2^e_s exactly.
+struct PartialScale {
+  float k;  // multiplier taking acc to the stored f16 values: 2^-e / l
+  int e;
+};
+template <int D>
+__device__ __forceinline__ PartialScale partial_scale(const f32x16 (&acc)[D / 32], float l_tot) {
+  constexpr int DT = D / 32;
+  float amax = 0.f;
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(acc[d][r]));
+  amax = xor32_max(amax);  // the row's other half of head_dim (lanes l and l ^ 32)
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  const float omax = amax * inv;
+  // frexp exponent: omax = f 2^e with f in [0.5, 1); 0 for a zero or
+  // non-finite row (whose values then pass through unscaled).
+  const int e = omax > 0.f && omax <= FLT_MAX ? __builtin_amdgcn_frexp_expf(omax) : 0;
+  return {__builtin_ldexpf(inv, -e), e};
+}
+
 // A lane's result for its query qi (row ``row`` of the work item's BM
-// queries): the output, or with split-KV the normalised partial in f16
-// (|value| <= max |v|, 11-bit mantissa) plus (reference, l) in fp32, which the
-// merge re-weights by l. No visible key: partial o = 0, reference -inf; final
-// output NaN (0 * inf), as the reference.
+// queries): the output, or with split-KV the scaled f16 partial and its fp32
+// record (partial_scale). No visible key: partial o = 0, reference -inf;
+// final output NaN (0 * inf), as the reference.
 template <int D, typename T>
 __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it, int bm, int row,
                                              int qi, int g, const f32x16 (&acc)[D / 32],
@@ -898,8 +981,7 @@ __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it,
       }
   } else {
     const int64_t pidx = it.pbase + it.split;
-    const bool any = l_tot > 0.f;
-    const float inv = any ? 1.0f / l_tot : 0.f;
+    const PartialScale ps = partial_scale<D>(acc, l_tot);
     uint16_t* po = a.ws_o + (pidx * bm + row) * D;
 #pragma unroll
     for (int d = 0; d < DT; ++d)
@@ -907,13 +989,13 @@ __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it,
       for (int r4 = 0; r4 < 4; ++r4) {
         const int dim = 32 * d + 8 * r4 + 4 * g;
         u32x2 w;
-        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
-        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
+        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
+        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
         *reinterpret_cast<u32x2*>(po + dim) = w;
       }
     if (g == 0)
-      *reinterpret_cast<float2*>(a.ws_ml + (pidx * bm + row) * 2) =
-          make_float2(any ? mref : -INFINITY, l_tot);
+      *reinterpret_cast<f32x4*>(a.ws_ml + (pidx * bm + row) * 4) =
+          f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
   }
 }
 
@@ -942,17 +1024,17 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   const bool wave_active = q0 + wave * 32 < a.Lq;
   const int cache_len = it.cache_len;
 
-  // Key range of the workgroup. Block starts are sorted ascending, so the
-  // visible end is non-decreasing in the query index: the first and last
-  // queries bound it. Workgroup-uniform (scalar) work, no barrier. The
+  // Key range of the workgroup: end_bounds over its first and last queries.
+  // Workgroup-uniform (scalar) work, no barrier. The
   // dual-stream (decode) path tiles the largest range any query of the chunk
   // can see (the whole cache and all Lq new keys) so that its tile loads go
   // out before the block starts are read; it skips the tiles past the
   // visible range and masks the straddling ones per key.
   int kv_min = 0, kv_max = cache_len + a.Lk;
   if (NS == 1) {
-    kv_min = cache_len + visible_end(a, q0);
-    kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
+    const EndBounds eb = end_bounds(a, q0, min(q0 + kBM, a.Lq) - 1);
+    kv_min = cache_len + eb.lo;
+    kv_max = cache_len + eb.hi;
   }
 
   const int n_ct = (cache_len + kBN - 1) / kBN;
@@ -1018,8 +1100,9 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     // The stream's first tile into registers right away. (Fetching the
     // second one too delays the first: a CU takes in 64 bytes per clock.)
     regs.load(ltid, src, t_first, t_first < t_end);
-    kv_min = cache_len + visible_end(a, q0);
-    kv_max = cache_len + visible_end(a, min(q0 + kBM, a.Lq) - 1);
+    const EndBounds eb = end_bounds(a, q0, min(q0 + kBM, a.Lq) - 1);
+    kv_min = cache_len + eb.lo;
+    kv_max = cache_len + eb.hi;
   }
 
   // Visible-key end of this lane's query (per-key masking of straddling tiles).
@@ -1369,8 +1452,9 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   const int cache_len = it.cache_len;
 
   // Key range of the workgroup (see attn_fwd_kernel).
-  const int kv_min = cache_len + visible_end(a, q0);
-  const int kv_max = cache_len + visible_end(a, min(q0 + BM, a.Lq) - 1);
+  const EndBounds eb = end_bounds(a, q0, min(q0 + BM, a.Lq) - 1);
+  const int kv_min = cache_len + eb.lo;
+  const int kv_max = cache_len + eb.hi;
   const int n_ct = (cache_len + kBN - 1) / kBN;
   const int n_tiles = n_ct + (kv_max - cache_len + kBN - 1) / kBN;
   // 32-bit unsigned: splits <= 16 and tiles < 2^26 (keys < 2^30), so the
@@ -1556,57 +1640,596 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   store_result<D, T>(a, it, BM, row, qi, g, acc, l_tot, mref);
 }
 
+// ---------------------------------------------------------------------------
+// Decode-shaped calls: split-KV in one launch.
+//
+// A work item is (batch, head, query group, key split). Its workgroup has NQW
+// waves, each owning 32 queries of the group (up to 32 NQW rows), and all of
+// them read every key tile of the split. On MI355X a CU takes in about
+// 50 GB/s whether the bytes come from HBM, L2 or LDS DMA, and the chip moves
+// bytes into CUs at about the HBM rate whatever their source, so every K/V
+// byte should reach exactly one CU: the planner keeps one query group where
+// it can and picks the splits from a cost model.
+//
+// Loads. A wave issues LDS DMA for its own Q rows, then its share of the
+// split's first kDecSlots K/V tiles (the swizzled unpadded layout of the
+// prefill kernel); a slot is refilled once every wave is done with its tile.
+// Memory instructions stall at issue once enough are in flight, so nothing
+// else is put between the first loads and the wait for them.
+//
+// No workgroup barrier in the tile loop: each wave waits for its own pieces
+// of a tile (a compile-time vmcnt: every wave issues the same count per
+// tile, dead tiles reading past their buffer), then counts itself in on the
+// slot's arrival counter in LDS and waits there for the other waves, so a
+// tile is computed as soon as its bytes have landed while later tiles stream
+// in.
+//
+// Merge. Each split stores its partial (partial_scale format), then either a
+// separate merge kernel combines them (attn_combine_kernel), or the splits
+// merge in the kernel itself: every split arrives on its group's counter and
+// merges one row chunk of all the group's partials once all have arrived.
+// ---------------------------------------------------------------------------
+constexpr int kMaxDecSplits = 8;
+// Merge state of each work-item group (arrival and finish counters, chunk
+// claims), indexed by the group's first partial, in a region of fixed size at
+// the start of every attention workspace, so that no plan's partials ever
+// overlap another plan's state. Zero before a launch, zero after it.
+constexpr int kCounterStride = 16;           // ints per group state (arrivals, finished, claims)
+constexpr int kCounterSlots = 4096;          // partials a decode launch may have
+constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
+// Poll limit of a workgroup waiting for its group's other splits:
+// s_memrealtime ticks (100 MHz), 50 us. Reached only when a split cannot be
+// scheduled; the last arrival then merges the waiting workgroup's rows.
+constexpr uint64_t kSpinTicks = 5000;
+static_assert(2 + kMaxDecSplits <= kCounterStride, "group state fits its slot");
+
+// K/V tile slots in LDS: four, or three where four tiles and the Q rows
+// would not fit (head_dim 128 with four query waves).
+template <int D, int NQW> struct DecSlots {
+  static constexpr int value = D == 128 && NQW == 4 ? 3 : 4;
+};
+
+template <int D, int NQW> struct DecLds {
+  static constexpr int SL = DecSlots<D, NQW>::value;
+  using L = PairLds<D, SL>;
+  static constexpr int q_off = L::bytes;      // Q rows, K-swizzled (wave w: rows 32 w..)
+  static constexpr int sync_off = q_off + 32 * NQW * D * 2;  // slot counters, merge flags
+  static constexpr int bytes = sync_off + 2 * SL * 4 + 16;
+  static_assert(bytes <= 160 * 1024, "decode LDS must fit one workgroup");
+};
+
+// The decode kernel's DMA: piece p of a K (or V) tile goes to wave p % NQW,
+// and each wave fetches its own 32 Q rows (loaded through LDS, not into
+// registers directly: the compiler cannot count the inline-assembly pieces,
+// so its own wait for a register load issued before them would wait for
+// them all). Lane l of a piece fills physical chunk l % CR of row l / CR and
+// fetches the logical chunk the swizzle puts there.
+template <int D, int NQW>
+struct DecDma {
+  static constexpr int SL = DecSlots<D, NQW>::value;
+  using L = PairLds<D, SL>;
+  static constexpr int CR = D / 8;                // 16-byte chunks per row
+  static constexpr int RPP = 64 / CR;             // rows per piece
+  static constexpr int PK = kBN / RPP;            // pieces per K (or V) tile
+  static constexpr int NK = PK / NQW;             // K (and V) pieces per wave and tile
+  static constexpr int NQ = 32 / RPP;             // Q pieces per wave (its 32 rows)
+  static constexpr int per_tile = 2 * NK;         // a wave's pieces per tile
+  static_assert(PK % NQW == 0, "even piece deal");
+  uint32_t on[2 * NK], dc[2 * NK];  // lane offset in its tile (new-key stride), cache-stride delta
+  uint32_t qo[NQ];                  // lane offset of its Q pieces
+
+  __device__ __forceinline__ void init(int wid, int lane, const KvSrc& src, int q_sl2) {
+#pragma unroll
+    for (int m = 0; m < 2 * NK; ++m) {
+      const int r = (wid + NQW * (m % NK)) * RPP + lane / CR, x = lane % CR;
+      const int c = m < NK ? x ^ L::kswz(r) : x ^ (4 * L::vswz(r));
+      const uint32_t sn = uint32_t(m < NK ? src.k_sl2 : src.v_sl2);
+      on[m] = uint32_t(r) * sn + uint32_t(c * 16);
+      dc[m] = uint32_t(r) * (uint32_t(src.c_ss2) - sn);
+    }
+#pragma unroll
+    for (int m = 0; m < NQ; ++m) {
+      const int r = wid * 32 + m * RPP + lane / CR, x = lane % CR;
+      qo[m] = uint32_t(r) * uint32_t(q_sl2) + uint32_t((x ^ L::kswz(r)) * 16);
+    }
+  }
+  // This wave's Q rows of the query group into the Q area.
+  __device__ __forceinline__ void issue_q(__amdgpu_buffer_rsrc_t rq, uint32_t lds_b, int wid) const {
+#pragma unroll
+    for (int m = 0; m < NQ; ++m)
+      dma_piece_at(rq, lds_b + DecLds<D, NQW>::q_off + (wid * NQ + m) * 1024, qo[m]);
+  }
+  // This wave's pieces of tile t (absolute index; dead when !live) into slot.
+  __device__ __forceinline__ void issue_tile(const KvSrc& src, uint32_t lds_b, int t, bool live,
+                                             int slot, int wid) const {
+    const bool in_cache = t < src.n_ct;
+    const __amdgpu_buffer_rsrc_t kc = src.kc, kn = src.kn, vc = src.vc, vn = src.vn;
+    const __amdgpu_buffer_rsrc_t rk = in_cache ? kc : kn, rv = in_cache ? vc : vn;
+    const uint32_t row0 = uint32_t((in_cache ? t : t - src.n_ct) * kBN);
+    const uint32_t bk = live ? row0 * uint32_t(in_cache ? src.c_ss2 : src.k_sl2) : 0x80000000u;
+    const uint32_t bv = live ? row0 * uint32_t(in_cache ? src.c_ss2 : src.v_sl2) : 0x80000000u;
+    const uint32_t cmask = in_cache ? ~0u : 0u;
+    const uint32_t kt = lds_b + 2 * L::kstage(slot), vt = lds_b + 2 * L::vstage(slot);
+#pragma unroll
+    for (int m = 0; m < NK; ++m) {
+      const uint32_t p = uint32_t(wid + NQW * m) * 1024u;
+      dma_piece_at(rk, kt + p, on[m] + (dc[m] & cmask) + bk);
+    }
+#pragma unroll
+    for (int m = 0; m < NK; ++m) {
+      const uint32_t p = uint32_t(wid + NQW * m) * 1024u;
+      dma_piece_at(rv, vt + p, on[NK + m] + (dc[NK + m] & cmask) + bv);
+    }
+  }
+};
+
+// One key tile for one wave from a slot: S^T = K Q^T, softmax, O^T += V^T P^T.
+// kb / vb: this lane's operand addresses in the slot (PairAddr plus the
+// slot's offset). The operand reads run ahead of the MFMAs that use them (K
+// fragments four MFMAs ahead, V^T fragments two), and sched_group_barrier
+// keeps that order: left to itself the compiler puts each read right before
+// its MFMA and the wave waits out the LDS latency every time.
+template <int D, typename T>
+__device__ __forceinline__ void dec_tile(const uint32_t (&kb)[D / 16], const uint32_t (&vb)[D / 32],
+                                         const u32x4 (&qr)[D / 16], f32x16 (&acc)[D / 32],
+                                         Softmax& sm, float c, int lim, bool masked) {
+  constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
+  constexpr int NQ = 2 * KS;  // S MFMAs: half i % 2 (keys 32 (i % 2)..), k-step i / 2
+  constexpr int NP = 4 * DT;  // PV MFMAs: key step i / DT, head_dim tile i % DT
+  constexpr int W = 4;        // K fragments in flight
+  auto kfrag = [&](int i) __attribute__((always_inline)) {
+    return lds_read_b128_at(kb[i / 2] + (i % 2) * 32 * RB);
+  };
+  auto vfrag = [&](int i) __attribute__((always_inline)) {
+    const uint32_t vu = vb[i % DT] + 16 * (i / DT) * RB;
+    const u32x2 lo = lds_read_tr16_at(vu);
+    const u32x2 hi = lds_read_tr16_at(vu + 8 * RB);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+  f32x16 s[2] = {f32x16{}, f32x16{}};
+  u32x4 kf[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i) kf[i] = kfrag(i);
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    s[i % 2] = Mfma<T>::run(kf[i % W], qr[i / 2], s[i % 2]);
+    if (i + W < NQ) kf[i % W] = kfrag(i + W);
+  }
+#pragma unroll
+  for (int i = 0; i < W; ++i) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 1, 0);
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    __builtin_amdgcn_sched_group_barrier(sg::kMfma, 1, 0);
+    if (i + W < NQ) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const float mb = softmax_max<D>(s, acc, sm, c, lim, masked);
+  u32x4 pk[4];
+  exp_pack<T>(s, sm, c, mb, pk);
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 vf[2];
+  vf[0] = vfrag(0);
+  vf[1] = vfrag(1);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    acc[i % DT] = Mfma<T>::run(vf[i % 2], pk[i / DT], acc[i % DT]);
+    if (i + 2 < NP) vf[i % 2] = vfrag(i + 2);
+  }
+  __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 4, 0);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    __builtin_amdgcn_sched_group_barrier(sg::kMfma, 1, 0);
+    if (i + 2 < NP) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 2, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Count this wave in on an LDS counter (once, from lane 0: an add from every
+// lane would be folded into one add of the lane count) after its own LDS
+// reads have completed, and wait until the counter reaches `target`. The other
+// waves of the workgroup count themselves in the same way; they are all
+// resident, so the wait ends.
+__device__ __forceinline__ void lds_rendezvous(int* ctr, int target) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+    __builtin_amdgcn_s_sleep(0);
+  asm volatile("" ::: "memory");
+}
+
+template <int D, typename T, int NQW>
+__global__ __launch_bounds__(64 * NQW, 1) void attn_decode_kernel(AttnArgs a) {
+  constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
+  constexpr int NT = 64 * NQW;
+  constexpr int kRows = 32 * NQW;
+  using DL = DecLds<D, NQW>;
+  constexpr int kDecSlots = DL::SL;
+  using L = PairLds<D, kDecSlots>;
+  using Dma = DecDma<D, NQW>;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  prefetch_args(a);
+
+  const Coord it = locate(a, blockIdx.x, false, 0);  // qtile: the query group
+  const int b = it.b, h = it.h;
+  const int wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int lane = int(threadIdx.x) & 63, g = lane >> 5, n = lane & 31;
+  const int q0 = it.qtile * a.bm;
+  const int q_end = min(q0 + a.bm, a.Lq);
+  const int row = wid * 32 + n;  // row within the query group
+  const int qi = q0 + row;
+  const bool qvalid = qi < q_end;
+  const bool wave_active = q0 + wid * 32 < q_end;
+  const int cache_len = it.cache_len;
+
+  // Tiles over every key any query of the call may see (cache, then all Lk
+  // new keys), so the loads go out before the block starts are read; tiles
+  // past this group's visible keys are skipped, straddling ones masked.
+  const int n_ct = (cache_len + kBN - 1) / kBN;
+  const int n_tiles = n_ct + (a.Lk + kBN - 1) / kBN;
+  const int t_begin = int(uint32_t(it.split) * uint32_t(n_tiles) / uint32_t(it.n_splits));
+  const int t_end = int(uint32_t(it.split + 1) * uint32_t(n_tiles) / uint32_t(it.n_splits));
+  const int nt = t_end - t_begin;
+
+  KvSrc src;
+  src.c_ss2 = int(a.c_ss) * 2;
+  src.k_sl2 = int(a.k_sl) * 2;
+  src.v_sl2 = int(a.v_sl) * 2;
+  src.n_ct = n_ct;
+  {
+    const int hk = a.kv_group == 1 ? h : h / a.kv_group;
+    const int64_t coff = b * a.c_sb + hk * a.c_sh;
+    src.kc = make_rsrc(a.ck ? a.ck + coff : a.q, cache_len, src.c_ss2, D);
+    src.vc = make_rsrc(a.cv ? a.cv + coff : a.q, cache_len, src.c_ss2, D);
+    src.kn = make_rsrc(a.k + b * a.k_sb + hk * a.k_sh, a.Lk, src.k_sl2, D);
+    src.vn = make_rsrc(a.v + b * a.v_sb + hk * a.v_sh, a.Lk, src.v_sl2, D);
+    src.none = make_rsrc(a.q, 0, 0, D);
+  }
+  const uint32_t smem_b = lds_addr(smem);
+  int* const sync = reinterpret_cast<int*>(reinterpret_cast<char*>(smem) + DL::sync_off);
+  if (threadIdx.x < 2 * kDecSlots) sync[threadIdx.x] = 0;
+  Dma dma;
+  dma.init(wid, lane, src, int(a.q_sl) * 2);
+  {
+    // This wave's Q rows of [q0, q_end) of head h; rows past them read as zeros.
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(a.q + b * a.q_sb + int64_t(q0) * a.q_sl + h * a.q_sh, q_end - q0,
+                  int(a.q_sl) * 2, D);
+    dma.issue_q(rq, smem_b, wid);
+  }
+#pragma unroll
+  for (int j = 0; j < kDecSlots; ++j) dma.issue_tile(src, smem_b, t_begin + j, j < nt, j, wid);
+  __syncthreads();  // the counters are zeroed before anyone counts in
+
+  const EndBounds eb = end_bounds(a, q0, q_end - 1);
+  const int kv_min = cache_len + eb.lo, kv_max = cache_len + eb.hi;
+  // Evaluated on every lane (rows past the group clamped): the block-start
+  // reads then stay scalar loads, which the tile waits below do not count.
+  const int my_end = qvalid ? cache_len + visible_end(a, min(qi, a.Lq - 1)) : 0;
+
+  PairAddr<D, kDecSlots> ad;
+  ad.init(smem_b, lane);
+  f32x16 acc[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
+  Softmax sm{-INFINITY, 0.f};
+  const float c = a.scale_log2;
+  u32x4 qr[KS];
+
+  // Tile j sits in slot j % kDecSlots. Every wave issues the same number of
+  // pieces per tile, and the refill of tile j + kDecSlots follows tile j, so
+  // when tile j is needed exactly kDecSlots - 1 tiles were issued after it.
+  constexpr int kLead = (kDecSlots - 1) * Dma::per_tile;
+  for (int j = 0; j < nt; ++j) {
+    const int slot = j % kDecSlots, use = j / kDecSlots + 1;
+    __builtin_amdgcn_s_waitcnt((kLead & 15) | ((kLead >> 4) << 14) | (7 << 4));  // vmcnt(kLead)
+    lds_rendezvous(sync + slot, NQW * use);  // every wave's pieces of tile j have landed
+    if (j == 0) {
+      // Q^T operand of this wave's 32 queries (lane: query n, head_dim
+      // [16 s + 8 g, +8) per k-step s), from its K-swizzled Q rows (which
+      // its own vmcnt wait above covers).
+      const uint32_t qb = DL::q_off + wid * 32 * RB - 2 * L::kstage(0);
+      const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qr[s] = lds_read_b128_at(ad.k[s] + qb) ^ flip;
+    }
+    const int tg = t_begin + j;
+    const bool in_cache = tg < n_ct;
+    const int j0 = in_cache ? tg * kBN : cache_len + (tg - n_ct) * kBN;
+    if (wave_active && j0 < kv_max) {
+      const uint32_t ko = 2 * L::kstage(slot), vo = 2 * (L::vstage(slot) - L::vstage(0));
+      uint32_t kb[KS], vb[DT];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kb[s] = ad.k[s] + ko;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) vb[d] = ad.v[d] + vo;
+      const int lim = (in_cache ? cache_len - j0 : my_end - j0) - 4 * g;
+      const bool masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
+      dec_tile<D, T>(kb, vb, qr, acc, sm, c, lim, masked);
+    }
+    // Refill the slot with tile j + kDecSlots once every wave is done with it.
+    lds_rendezvous(sync + kDecSlots + slot, NQW * use);
+    dma.issue_tile(src, smem_b, tg + kDecSlots, j + kDecSlots < nt, slot, wid);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the last (dead) pieces land before the LDS is reused
+  __syncthreads();
+
+  const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
+  const float l_tot = xor32_sum(sm.l);
+  if (it.n_splits == 1) {
+    if (qvalid) store_result<D, T>(a, it, a.bm, row, qi, g, acc, l_tot, mref);
+    return;
+  }
+
+  // Partial of this split: values [split][row][D] and records [split][row]
+  // of the group's workspace area. The lanes hold scattered 8-byte runs of
+  // 32 rows, so the partial is staged in LDS (rows padded by 16 bytes) and
+  // stored as whole rows, 16 bytes per lane: device-scope write-through (sc1)
+  // when the splits merge in this kernel, plain stores for the merge kernel.
+  const bool in_kernel_merge = a.counters != nullptr;
+  const int nrows = q_end - q0;
+  const uint32_t ws_rows = uint32_t(a.bm);
+  const __amdgpu_buffer_rsrc_t rws =
+      __builtin_amdgcn_make_buffer_rsrc(a.ws_o + it.pbase * ws_rows * D, (short)0,
+                                        int(it.n_splits * ws_rows * D * 2), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + it.pbase * ws_rows * 4, (short)0, int(it.n_splits * ws_rows * 16), kBufWord3);
+  constexpr int kSc1 = 16;  // cache policy: device scope
+  constexpr int CR = D / 8;
+  constexpr int SP = 2 * D + 16;  // staging row pitch (bytes)
+  static_assert(kRows * (SP + 16) <= L::bytes, "staging fits the tile slots");
+  char* const stage = reinterpret_cast<char*>(smem);
+  f32x4* const srec = reinterpret_cast<f32x4*>(stage + kRows * SP);
+  if (qvalid) {
+    const PartialScale ps = partial_scale<D>(acc, l_tot);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int dim = 32 * d + 8 * r4 + 4 * g;
+        u32x2 w;
+        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
+        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
+        *reinterpret_cast<u32x2*>(stage + row * SP + dim * 2) = w;
+      }
+    if (g == 0) srec[row] = f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
+  }
+  __syncthreads();
+  for (int u = int(threadIdx.x); u < nrows * CR; u += NT) {
+    const int r = u / CR, ch = u - r * CR;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * SP + ch * 16);
+    const uint32_t off = ((uint32_t(it.split) * ws_rows + uint32_t(r)) * D + ch * 8) * 2;
+    if (in_kernel_merge) __builtin_amdgcn_raw_buffer_store_b128(v, rws, off, 0, kSc1);
+    else __builtin_amdgcn_raw_buffer_store_b128(v, rws, off, 0, 0);
+  }
+  for (int r = int(threadIdx.x); r < nrows; r += NT) {
+    const u32x4 v = __builtin_bit_cast(u32x4, srec[r]);
+    const uint32_t off = (uint32_t(it.split) * ws_rows + uint32_t(r)) * 16;
+    if (in_kernel_merge) __builtin_amdgcn_raw_buffer_store_b128(v, rrec, off, 0, kSc1);
+    else __builtin_amdgcn_raw_buffer_store_b128(v, rrec, off, 0, 0);
+  }
+  if (!in_kernel_merge) return;
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete at device scope
+  __syncthreads();
+
+  // Merge, spread over the group: split s merges row chunk s (rows
+  // [s nrows / S, (s + 1) nrows / S)) of every split's partial, once all S
+  // partials are stored. Group state, at the group's counter slot:
+  //   gs[0] arrivals, gs[1] workgroups finished with the state, gs[2 + c]
+  //   chunk c claimed.
+  // A workgroup arrives (gs[0] += 1); unless it is the last arrival it polls
+  // gs[0] until all S have arrived, with a time limit, so it never waits
+  // forever on a workgroup that has not been scheduled (one whose CU it
+  // holds). A chunk is merged by whoever claims it first (compare-and-swap):
+  // its owner once all have arrived, or the last arrival, which after its
+  // own chunk claims every chunk still unclaimed -- those of owners that
+  // gave up or have not yet seen the last arrival. Every chunk is therefore
+  // merged exactly once, whatever the schedule. The last workgroup to finish
+  // resets the state to zero for the next call.
+  const int S = it.n_splits;
+  int32_t* const gs = a.counters + it.pbase * kCounterStride;
+  int* const sh = sync + 2 * kDecSlots;
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(gs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == S - 1;
+    int all = last;
+    if (!last) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      for (;;) {
+        if (__hip_atomic_fetch_add(gs, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= S) {
+          all = 1;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    sh[0] = all;
+    sh[1] = last;
+  }
+  __syncthreads();
+  const bool all = sh[0] != 0, last = sh[1] != 0;
+  // A chunk has at most kRows / 2 rows (S >= 2). Per chunk: every record and
+  // value load goes out at once; the records go to LDS, where one thread per
+  // row turns them into the row's split weights, and each thread combines its
+  // units (row, 8-dim chunk) from the values it holds.
+  constexpr int UPT = (kRows / 2 * CR + NT - 1) / NT;  // units per thread
+  constexpr int RPT = (kMaxDecSplits * kRows / 2 + NT - 1) / NT;  // records per thread
+  f32x4* const lrec = reinterpret_cast<f32x4*>(smem);                       // [split][row]
+  float* const lcoef = reinterpret_cast<float*>(lrec + kMaxDecSplits * kRows / 2);  // [row][split]
+  int* const lexp = reinterpret_cast<int*>(lcoef + kRows / 2 * kMaxDecSplits);     // [row]
+  static_assert(kMaxDecSplits * kRows / 2 * 20 + kRows / 2 * 4 <= L::bytes, "merge scratch fits");
+  for (int c0 = 0; all && c0 < (last ? S : 1); ++c0) {
+    const int c = it.split + c0 < S ? it.split + c0 : it.split + c0 - S;  // own chunk first
+    __syncthreads();  // the previous chunk's LDS scratch and sh[2] have been read
+    if (threadIdx.x == 0) {
+      int unclaimed = 0;
+      sh[2] = __hip_atomic_compare_exchange_strong(gs + 2 + c, &unclaimed, 1, __ATOMIC_RELAXED,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!sh[2]) continue;
+    const int r_lo = c * nrows / S, rn = (c + 1) * nrows / S - r_lo;
+    f32x4 rv[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int idx = int(threadIdx.x) + NT * i, sp = idx / (kRows / 2), r = idx % (kRows / 2);
+      if (sp < S && r < rn)
+        rv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rrec, (uint32_t(sp) * ws_rows + r_lo + r) * 16, 0, kSc1));
+    }
+    u32x4 val[UPT][kMaxDecSplits];
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      const int u = int(threadIdx.x) + NT * k, r = u / CR, ch = u % CR;
+#pragma unroll
+      for (int sp = 0; sp < kMaxDecSplits; ++sp)
+        if (sp < S && r < rn)
+          val[k][sp] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rws, ((uint32_t(sp) * ws_rows + r_lo + r) * D + ch * 8) * 2, 0, kSc1));
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int idx = int(threadIdx.x) + NT * i, sp = idx / (kRows / 2), r = idx % (kRows / 2);
+      if (sp < S && r < rn) lrec[sp * (kRows / 2) + r] = rv[i];
+    }
+    __syncthreads();
+    if (int(threadIdx.x) < rn) {
+      // Row weights: c_s = exp2(m_s - M) l_s / L, taken relative to the largest
+      // scale exponent E (applied once at the end).
+      const int r = int(threadIdx.x);
+      float mmax = -INFINITY;
+      int emax = INT_MIN;
+      for (int sp = 0; sp < S; ++sp) {
+        mmax = fmaxf(mmax, lrec[sp * (kRows / 2) + r][0]);
+        emax = max(emax, int(lrec[sp * (kRows / 2) + r][2]));
+      }
+      const float base = mmax == -INFINITY ? 0.f : mmax;
+      float Lsum = 0.f;
+      for (int sp = 0; sp < S; ++sp) {
+        const f32x4 rs = lrec[sp * (kRows / 2) + r];
+        Lsum += fast_exp2(rs[0] - base) * rs[1];
+      }
+      const float invL = 1.0f / Lsum;  // no visible key anywhere: NaN, as the reference
+      for (int sp = 0; sp < S; ++sp) {
+        const f32x4 rs = lrec[sp * (kRows / 2) + r];
+        lcoef[r * kMaxDecSplits + sp] =
+            __builtin_ldexpf(fast_exp2(rs[0] - base) * rs[1] * invL, int(rs[2]) - emax);
+      }
+      lexp[r] = emax;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      const int u = int(threadIdx.x) + NT * k, r = u / CR, ch = u % CR;
+      if (r >= rn) continue;
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sp = 0; sp < kMaxDecSplits; ++sp)
+        if (sp < S) {
+          const float cs = lcoef[r * kMaxDecSplits + sp];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[2 * e] += cs * to_f32(f16_t{uint16_t(val[k][sp][e] & 0xffffu)});
+            o[2 * e + 1] += cs * to_f32(f16_t{uint16_t(val[k][sp][e] >> 16)});
+          }
+        }
+      const int emax = lexp[r];
+      u32x4 packed;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        packed[e] =
+            Mfma<T>::pack(__builtin_ldexpf(o[2 * e], emax), __builtin_ldexpf(o[2 * e + 1], emax));
+      uint16_t* op = a.out + b * a.o_sb + int64_t(q0 + r_lo + r) * a.o_sl + h * a.o_sh + ch * 8;
+      __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(op));
+    }
+  }
+  if (threadIdx.x == 0) {
+    // Done with the group's state; the last to get here resets it.
+    if (__hip_atomic_fetch_add(gs + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1) {
+      for (int i = 0; i < 2 + S; ++i)
+        __hip_atomic_store(gs + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 template <int D> struct CombineShape {
   static constexpr int TPR = D / 4;      // threads per row
   static constexpr int RPB = 256 / TPR;  // rows per block
 };
 
-// Merge split-KV partials: out = sum_s w_s acc_s / sum_s w_s l_s with
-// w_s = exp2(m_s - max_s m_s). Each thread owns 4 consecutive dims of a row
-// and issues every load it needs before combining. Blocks of one
-// (batch, head) run on the XCD whose L2 holds that head's partials.
+// Merge of n split-KV partials of one row (records ml, stored values o, one
+// 16-byte record and 4 f16 values per split) into 4 output values:
+//   out = sum_s c_s o_s 2^e_s,  c_s = exp2(m_s - M) l_s / L,  L = sum_s exp2(m_s - M) l_s
+// with M the largest m_s. The sum runs relative to E, the largest e_s, and
+// 2^E is applied once at the end: every coefficient c_s 2^(e_s - E) is <= 1,
+// so no intermediate overflows, and |out| <= max |v| as in the reference. No
+// visible key in any split: L = 0 and the output is NaN, as the reference.
+template <int NMAX>
+__device__ __forceinline__ f32x4 merge_partials(const f32x4 (&ml)[NMAX], const u32x2 (&o)[NMAX],
+                                                int n) {
+  float mmax = -INFINITY;
+  int emax = INT_MIN;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s)
+    if (s < n) {
+      mmax = fmaxf(mmax, ml[s][0]);
+      emax = max(emax, int(ml[s][2]));
+    }
+  const float base = mmax == -INFINITY ? 0.f : mmax;
+  float w[NMAX];
+  float L = 0.f;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s)
+    if (s < n) {
+      w[s] = fast_exp2(ml[s][0] - base) * ml[s][1];
+      L += w[s];
+    }
+  const float invL = 1.0f / L;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s)
+    if (s < n) {
+      const float c = __builtin_ldexpf(w[s] * invL, int(ml[s][2]) - emax);
+      acc[0] += c * to_f32(f16_t{uint16_t(o[s][0] & 0xffffu)});
+      acc[1] += c * to_f32(f16_t{uint16_t(o[s][0] >> 16)});
+      acc[2] += c * to_f32(f16_t{uint16_t(o[s][1] & 0xffffu)});
+      acc[3] += c * to_f32(f16_t{uint16_t(o[s][1] >> 16)});
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = __builtin_ldexpf(acc[e], emax);
+  return acc;
+}
+
+// Merge split-KV partials (merge_partials). Each thread owns 4 consecutive
+// dims of a row and issues every load it needs before combining. Blocks of
+// one (batch, head) run on the XCD whose L2 holds that head's partials.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   prefetch_args(a);
   using CS = CombineShape<D>;
-  const Coord cd = locate(a, blockIdx.x, true, a.bm / CS::RPB);
+  // Blocks per work-item group: ceil(bm / RPB), as the host sizes the grid
+  // (bm need not be a multiple of RPB: decode query groups).
+  const Coord cd = locate(a, blockIdx.x, true, (a.bm + CS::RPB - 1) / CS::RPB);
   const int row = cd.split * CS::RPB + threadIdx.x / CS::TPR;
   const int dim = 4 * (threadIdx.x % CS::TPR);
   const int qi = cd.qtile * a.bm + row;
-  if (qi >= a.Lq) return;
-  float2 ml[kMaxSplits];
+  if (row >= a.bm || qi >= a.Lq) return;
+  f32x4 ml[kMaxSplits];
   u32x2 o[kMaxSplits];
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
     if (s < cd.n_splits) {
-      ml[s] = *reinterpret_cast<const float2*>(a.ws_ml + ((cd.pbase + s) * a.bm + row) * 2);
+      ml[s] = *reinterpret_cast<const f32x4*>(a.ws_ml + ((cd.pbase + s) * a.bm + row) * 4);
       o[s] = *reinterpret_cast<const u32x2*>(a.ws_o + ((cd.pbase + s) * a.bm + row) * D + dim);
     }
   }
-  float mmax = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s)
-    if (s < cd.n_splits) mmax = fmaxf(mmax, ml[s].x);
-  const float base = mmax == -INFINITY ? 0.f : mmax;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-#pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
-    if (s < cd.n_splits) {
-      // Weight of split s: its exponent offset times its own sum (o_s is normalised).
-      const float w = fast_exp2(ml[s].x - base) * ml[s].y;
-      l += w;
-      acc[0] += w * to_f32(f16_t{uint16_t(o[s][0] & 0xffffu)});
-      acc[1] += w * to_f32(f16_t{uint16_t(o[s][0] >> 16)});
-      acc[2] += w * to_f32(f16_t{uint16_t(o[s][1] & 0xffffu)});
-      acc[3] += w * to_f32(f16_t{uint16_t(o[s][1] >> 16)});
-    }
-  }
-  const float inv = 1.0f / l;  // no visible key anywhere: 0 * inf = NaN, as the reference
+  const f32x4 acc = merge_partials(ml, o, cd.n_splits);
   uint16_t* op = a.out + cd.b * a.o_sb + int64_t(qi) * a.o_sl + cd.h * a.o_sh + dim;
   u32x2 w2;
-  w2[0] = Mfma<T>::pack(acc[0] * inv, acc[1] * inv);
-  w2[1] = Mfma<T>::pack(acc[2] * inv, acc[3] * inv);
+  w2[0] = Mfma<T>::pack(acc[0], acc[1]);
+  w2[1] = Mfma<T>::pack(acc[2], acc[3]);
   __builtin_nontemporal_store(w2, reinterpret_cast<u32x2*>(op));
 }
 
@@ -1630,14 +2253,20 @@ int device_cus() {
   return cache[dev];
 }
 
+// Attention kernels a plan can pick (the DX_TUNE_ATTN_KERNEL values).
+enum AttnKernel { kSingle = 1, kDual = 2, kPaired = 3, kDecode = 4 };
+
 struct Plan {
   int n_qtiles;
-  int bm;                    // queries per work item
-  int streams;               // 2: dual-stream decode, 1: single stream, 3: paired groups
+  int bm;                    // queries per work item (decode: query-group rows)
+  int kernel;                // AttnKernel
+  int nqw;                   // decode: query waves per workgroup (2 or 4)
+  bool merge_kernel;         // decode: splits merged by attn_combine_kernel, not in the kernel
   int n_seg;                 // 0 = uniform
   int uniform_splits;
   std::vector<int> seg_b, seg_splits, seg_cache, seg_base, comb_base;
   int64_t items, comb_blocks, partials;
+  int64_t counter_bytes;     // decode: arrival counters at the start of the workspace
   int64_t ws_bytes;
 };
 
@@ -1647,133 +2276,222 @@ int64_t combine_bpt(int64_t D, int64_t bm) {
   return cdiv(bm, D == 128 ? CombineShape<128>::RPB : CombineShape<64>::RPB);
 }
 
-long split_override() {  // DX_ATTN_SPLITS=<n>: tuning override (measurement only)
-  const char* env = getenv("DX_ATTN_SPLITS");
-  return env ? strtol(env, nullptr, 10) : 0;
-}
+int bm_of(int kernel) { return kernel == kPaired ? kBMPair : kBM; }
 
-// DX_ATTN_STREAMS=1|2|3 (single stream / dual-stream / paired groups):
-// tuning override (measurement only).
-long streams_override() {
-  const char* env = getenv("DX_ATTN_STREAMS");
-  const long v = env ? strtol(env, nullptr, 10) : 0;
-  return v >= 1 && v <= 3 ? v : 0;
-}
-
-int bm_of(int streams) { return streams == 3 ? kBMPair : kBM; }
-
-// Split count for `groups` (batch, head, query tile) units of `tiles` key
-// tiles each. Decode-shaped calls (few groups, long key range) get
-// dual-stream workgroups on about three quarters of the CUs: measured at the
-// Wan-5B chunk shape (24 groups, 22 tiles), 8 splits beat 10 (one per CU)
-// because the merge reads 20% fewer partials while the loads, spread over
-// 192 CUs, finish as fast. Otherwise the split minimising rounds x
-// tiles-per-split (two workgroups per CU) with a small cost per extra split
-// (partials + merge).
-int choose_uniform_splits(int64_t units, int64_t Lq, int64_t tiles, int cus, int& streams) {
-  // units: (batch, head) pairs. Decode-shaped at 128 queries per item?
-  const int64_t groups128 = units * cdiv(Lq, kBM);
-  int64_t best_s = 1;
-  if (groups128 * 2 <= cus && tiles >= 4) {
-    streams = 2;
-    best_s = std::max<int64_t>(1, std::min<int64_t>({kMaxSplits, (3 * cus) / (4 * groups128),
-                                                      cdiv(tiles, 2)}));
-  } else {
-    // Paired groups: 256 queries per workgroup, one workgroup per CU; the
-    // split minimising rounds x (tiles per split + a fixed cost per work
-    // item, about 8 tiles: its start-up, its stores, and the K/V its key
-    // range pulls that another query tile of the head already read), plus
-    // 2 tiles per split for partials and merge. Calibrated at the Wan-14B
-    // chunk (160 groups of 130 tiles): measured 1..10 splits order as this
-    // cost does, 3 best (179 us, against 208 us at 8 and 188 us at 1).
-    streams = 3;
-    const int64_t groups = units * cdiv(Lq, kBMPair);
-    if (groups < 2 * cus && tiles >= 8) {
-      double best = 1e30;
-      for (int64_t s = 1; s <= kMaxSplits && s <= tiles / 4; ++s) {
-        const double cost = double(cdiv(groups * s, cus)) * double(cdiv(tiles, s) + 8) +
-                            (s > 1 ? 2.0 * double(s) : 0.0);
-        if (cost < best - 1e-9) { best = cost; best_s = s; }
+// Query-group rows and per-segment key splits of the one-launch decode
+// kernel, for segments of `units` (batch, head) pairs over tiles[i] key tiles
+// each (a uniform call is one segment of B*H units). Modelled time (us): a
+// CU streams ~50 GB/s whatever the source (HBM, L2, LDS DMA: measured on
+// MI355X) and the chip ~6 TB/s, so the streaming phase is the larger of the
+// worst split's bytes per CU and the call's HBM bytes over the chip; the
+// merge adds ~1.2 us (stores, arrival, polling) plus each split's read of
+// its row chunk of every split's partial. Candidates keep at most one
+// workgroup per CU. rows == 0: no
+// candidate fits (prefill-shaped: the paired kernel takes it).
+struct DecodeShape {
+  int rows = 0, nqw = 0;
+  std::vector<int> splits;
+};
+DecodeShape choose_decode(int64_t units, int64_t Lq, const std::vector<int64_t>& tiles, int64_t D,
+                          int cus, int forced_splits) {
+  constexpr double kCuBytesPerUs = 50e3, kChipBytesPerUs = 6e6, kMergeFixedUs = 1.2;
+  const int64_t tile_bytes = int64_t(kBN) * D * 2 * 2;
+  int64_t all_tiles = 0, max_tiles = 1;
+  for (int64_t t : tiles) {
+    all_tiles += t;
+    max_tiles = std::max(max_tiles, t);
+  }
+  // Every query group reads its splits' K/V, and the chip moves bytes into
+  // CUs (from L2 as from HBM) at about the HBM rate: query groups multiply it.
+  const double t_chip1 = double(units * all_tiles * tile_bytes) / kChipBytesPerUs;
+  DecodeShape best;
+  double best_cost = 1e30;
+  for (int64_t nq = cdiv(Lq, 128); nq <= cdiv(Lq, 16); ++nq) {
+    const int64_t rows = cdiv(Lq, nq);
+    if (nq > 1 && cdiv(Lq, cdiv(Lq, nq - 1)) == nq) continue;  // same groups as nq - 1
+    // Largest split per segment: cap on the tiles one workgroup streams.
+    for (int64_t cap = max_tiles; cap >= 1; --cap) {
+      std::vector<int> sp(tiles.size());
+      int64_t wgs = 0;
+      double worst = 0.0, merge = 0.0;
+      bool ok = true;
+      for (size_t i = 0; i < tiles.size(); ++i) {
+        const int64_t ti = std::max<int64_t>(tiles[i], 1);
+        int64_t si = forced_splits ? std::min<int64_t>(forced_splits, ti) : cdiv(ti, cap);
+        if (si > kMaxDecSplits) ok = false;
+        si = std::min<int64_t>(si, kMaxDecSplits);
+        sp[i] = int(si);
+        wgs += units * nq * si;
+        worst = std::max(worst, double(cdiv(ti, si) * tile_bytes + rows * D * 2) / kCuBytesPerUs);
+        // Split s merges rows chunk s of every split's partial.
+        if (si > 1)
+          merge = std::max(merge, kMergeFixedUs + double(cdiv(rows, si) * si * (D * 2 + 16)) /
+                                                      kCuBytesPerUs);
       }
+      if (!ok || wgs > cus) break;  // a smaller cap only needs more workgroups
+      const double cost = std::max(worst, t_chip1 * double(nq)) + merge;
+      if (cost < best_cost - 1e-9) {
+        best_cost = cost;
+        best.rows = int(rows);
+        best.nqw = rows <= 64 ? 2 : 4;
+        best.splits = sp;
+      }
+      if (forced_splits) break;  // one candidate per query grouping
     }
   }
-  const long forced = split_override();
-  if (forced >= 1) best_s = forced;
-  if (streams_override()) streams = int(streams_override());
-  return int(std::max<int64_t>(1, std::min<int64_t>({best_s, kMaxSplits,
-                                                     std::max<int64_t>(tiles, 1)})));
+  return best;
+}
+
+// Paired-group (prefill) split count for `groups` (batch, head, 256-query
+// tile) units of `tiles` key tiles each: the split minimising rounds x
+// (tiles per split + a fixed cost per work item, about 8 tiles: its
+// start-up, its stores, and the K/V its key range pulls that another query
+// tile of the head already read), plus 2 tiles per split for partials and
+// merge. Calibrated at the Wan-14B chunk (160 groups of 130 tiles): measured
+// 1..10 splits order as this cost does, 3 best (179 us, against 208 us at 8
+// and 188 us at 1).
+int choose_paired_splits(int64_t groups, int64_t tiles, int cus) {
+  int64_t best_s = 1;
+  if (groups < 2 * cus && tiles >= 8) {
+    double best = 1e30;
+    for (int64_t s = 1; s <= kMaxSplits && s <= tiles / 4; ++s) {
+      const double cost = double(cdiv(groups * s, cus)) * double(cdiv(tiles, s) + 8) +
+                          (s > 1 ? 2.0 * double(s) : 0.0);
+      if (cost < best - 1e-9) { best = cost; best_s = s; }
+    }
+  }
+  return int(best_s);
 }
 
 Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t cache_len,
                const int64_t* cache_lens) {
   Plan p{};
   const int cus = device_cus();
-  if (!cache_lens) {
-    const int64_t tiles = cdiv(cache_len, kBN) + cdiv(Lk, kBN);
-    p.uniform_splits = choose_uniform_splits(B * H, Lq, tiles, cus, p.streams);
-    p.bm = bm_of(p.streams);
-    p.n_qtiles = int(cdiv(Lq, p.bm));
-    const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
-    p.items = B * per_b * p.uniform_splits;
-    p.partials = p.uniform_splits > 1 ? p.items : 0;
-    p.comb_blocks = p.uniform_splits > 1 ? B * per_b * combine_bpt(D, p.bm) : 0;
-  } else {
-    // One segment per sequence, longest first, with splits proportional to
-    // its length: within one dual-stream workgroup per CU when that leaves
-    // <= 8 tiles per split, else within two single-stream workgroups per CU.
-    std::vector<int> order(B);
-    for (int i = 0; i < int(B); ++i) order[i] = i;
+  const int forced_kernel = tuning(DX_TUNE_ATTN_KERNEL);
+  const int forced_splits = tuning(DX_TUNE_ATTN_SPLITS);
+  // Segments: one per sequence of a ragged batch, longest first; a uniform
+  // call is one segment of all B*H (batch, head) pairs.
+  const int nseg = cache_lens ? int(B) : 1;
+  std::vector<int> order(nseg);
+  std::vector<int64_t> tiles(nseg);
+  for (int i = 0; i < nseg; ++i) order[i] = i;
+  if (cache_lens)
     std::stable_sort(order.begin(), order.end(),
                      [&](int x, int y) { return cache_lens[x] > cache_lens[y]; });
-    std::vector<int64_t> tiles(B);
+  for (int k = 0; k < nseg; ++k) {
+    const int64_t c = cache_lens ? cache_lens[order[k]] : cache_len;
+    tiles[k] = cdiv(c, kBN) + cdiv(Lk, kBN);
+  }
+  const int64_t units = cache_lens ? H : B * H;  // (batch, head) pairs per segment
+
+  std::vector<int> splits(nseg, 1);
+  // The one-launch decode kernel is opt-in (DX_TUNE_ATTN_KERNEL = 4): on the
+  // C1 decode chunk it measures 16-22 us against 14.5 us for the dual-stream
+  // kernel and its merge kernel.
+  DecodeShape dec;
+  if (forced_kernel == kDecode && forced_splits <= kMaxDecSplits)
+    dec = choose_decode(units, Lq, tiles, D, cus, forced_splits);
+  if (forced_kernel == kDecode && dec.rows == 0) {
+    // Forced onto the decode kernel: the smallest query groups that fit the
+    // kernel, splits as forced (or 1), however many workgroups that takes.
+    dec.rows = int(std::min<int64_t>(Lq, 128));
+    dec.nqw = dec.rows <= 64 ? 2 : 4;
+    dec.splits.assign(nseg, 1);
+    for (int k = 0; k < nseg; ++k)
+      dec.splits[k] = int(std::max<int64_t>(1, std::min<int64_t>({forced_splits ? forced_splits : 1,
+                                                                  kMaxDecSplits, tiles[k]})));
+  }
+  if (dec.rows > 0) {
+    int64_t items = 0;
+    for (int k = 0; k < nseg; ++k) items += units * cdiv(Lq, dec.rows) * dec.splits[k];
+    if (items > kCounterSlots) dec.rows = 0;  // too many groups for the counter region
+  }
+  if (dec.rows > 0) {
+    p.kernel = kDecode;
+    p.bm = dec.rows;
+    p.nqw = dec.nqw;
+    p.merge_kernel = tuning(DX_TUNE_ATTN_MERGE) == 2;
+    splits = dec.splits;
+  } else {
     int64_t total = 0;
-    for (int i = 0; i < int(B); ++i) {
-      tiles[i] = cdiv(cache_lens[i], kBN) + cdiv(Lk, kBN);
-      total += tiles[i];
-    }
-    // Dual-stream decode items (128 queries, one workgroup per CU) when that
-    // leaves <= 8 tiles per split, else paired-group items (256 queries, one
-    // workgroup per CU).
-    std::vector<int> splits(B, 1);
-    for (int streams : {2, 3}) {
-      const int64_t per_b = H * cdiv(Lq, bm_of(streams));
-      const double budget = double(cus) / double(per_b);
-      int64_t worst = 0;
-      for (int i = 0; i < int(B); ++i) {
-        int64_t s = int64_t(budget * double(tiles[i]) / double(std::max<int64_t>(total, 1)));
-        s = std::max<int64_t>(1, std::min<int64_t>({s, kMaxSplits, tiles[i]}));
-        splits[i] = int(s);
-        worst = std::max(worst, cdiv(tiles[i], s));
+    for (int64_t t : tiles) total += t;
+    if (forced_kernel && forced_kernel != kDecode) {
+      p.kernel = forced_kernel;
+    } else {
+      // Decode-shaped calls take the dual-stream kernel (128-query items, one
+      // workgroup per CU): a uniform call when its 128-query groups fill at
+      // most half the CUs, a ragged batch when splits in proportion to length
+      // leave <= 8 tiles per split. Everything else takes paired groups.
+      const int64_t g128 = units * cdiv(Lq, kBM);
+      bool dual;
+      if (nseg == 1) {
+        dual = g128 * 2 <= cus && tiles[0] >= 4;
+      } else {
+        int64_t worst = 0;
+        for (int k = 0; k < nseg; ++k) {
+          int64_t s = int64_t(double(cus) / double(g128) * double(tiles[k]) /
+                              double(std::max<int64_t>(total, 1)));
+          s = std::max<int64_t>(1, std::min<int64_t>({s, kMaxSplits, std::max<int64_t>(tiles[k], 1)}));
+          worst = std::max(worst, cdiv(tiles[k], s));
+        }
+        dual = worst <= 8;
       }
-      p.streams = streams;
-      if (streams == 2 && worst <= 8) break;
+      p.kernel = dual ? kDual : kPaired;
     }
-    if (streams_override()) p.streams = int(streams_override());
-    const long forced = split_override();
-    if (forced >= 1)
-      for (int i = 0; i < int(B); ++i)
-        splits[i] = int(std::max<int64_t>(1, std::min<int64_t>({forced, kMaxSplits, tiles[i]})));
-    p.bm = bm_of(p.streams);
-    p.n_qtiles = int(cdiv(Lq, p.bm));
-    const int64_t per_b = H * p.n_qtiles;
+    p.bm = bm_of(p.kernel);
+    const int64_t groups = units * cdiv(Lq, p.bm);  // work-item groups per segment
+    for (int k = 0; k < nseg; ++k) {
+      int64_t sk;
+      if (forced_splits)
+        sk = forced_splits;
+      else if (nseg > 1)  // ragged: splits in proportion to length, about one item per CU
+        sk = int64_t(double(cus) / double(groups) * double(tiles[k]) / double(std::max<int64_t>(total, 1)));
+      else if (p.kernel == kDual)  // about three quarters of the CUs, >= 2 tiles per split
+        sk = std::min<int64_t>((3 * cus) / (4 * groups), cdiv(tiles[k], 2));
+      else
+        sk = choose_paired_splits(groups, tiles[k], cus);
+      splits[k] = int(std::max<int64_t>(
+          1, std::min<int64_t>({sk, kMaxSplits, std::max<int64_t>(tiles[k], 1)})));
+    }
+  }
+  p.n_qtiles = int(cdiv(Lq, p.bm));
+  const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
+  if (!cache_lens) {
+    p.n_seg = 0;
+    p.uniform_splits = splits[0];
+    p.items = B * per_b * p.uniform_splits;
+    p.partials = p.uniform_splits > 1 ? p.items : 0;
+    const bool combine = p.kernel != kDecode || p.merge_kernel;
+    p.comb_blocks = p.uniform_splits > 1 && combine ? B * per_b * combine_bpt(D, p.bm) : 0;
+  } else {
     p.n_seg = int(B);
     p.seg_base.push_back(0);
     p.comb_base.push_back(0);
-    for (int k = 0; k < int(B); ++k) {
+    bool any_split = false;
+    for (int k = 0; k < nseg; ++k) {
       const int b = order[k];
       p.seg_b.push_back(b);
-      p.seg_splits.push_back(splits[b]);
+      p.seg_splits.push_back(splits[k]);
       p.seg_cache.push_back(int(cache_lens[b]));
-      p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[b]));
-      p.comb_base.push_back(
-          int(p.comb_base.back() + (splits[b] > 1 ? per_b * combine_bpt(D, p.bm) : 0)));
+      p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[k]));
+      const bool combine = p.kernel != kDecode || p.merge_kernel;
+      p.comb_base.push_back(int(p.comb_base.back() + (splits[k] > 1 && combine
+                                                          ? per_b * combine_bpt(D, p.bm) : 0)));
+      any_split = any_split || splits[k] > 1;
     }
     p.items = p.seg_base.back();
     p.comb_blocks = p.comb_base.back();
-    p.partials = p.items;
+    p.partials = any_split ? p.items : 0;
   }
-  // f16 partial outputs, then fp32 (reference, sum) pairs.
-  p.ws_bytes = p.comb_blocks > 0 ? p.partials * p.bm * (D * 2 + 2 * int64_t(sizeof(float))) : 0;
+  // Workspace of any plan with partials: the counter region (kCounterRegion
+  // bytes, used by the decode kernel only), the f16 partial values, then the
+  // fp32 records {m, l, e, 0}.
+  const bool has_partials = p.kernel == kDecode ? p.partials > 0 : p.comb_blocks > 0;
+  // The counters are the in-kernel merge's; the merge kernel needs none.
+  p.counter_bytes = has_partials ? kCounterRegion : 0;
+  p.ws_bytes = has_partials
+                   ? kCounterRegion + p.partials * p.bm * (D * 2 + 4 * int64_t(sizeof(float)))
+                   : 0;
   return p;
 }
 
@@ -1814,11 +2532,25 @@ hipError_t launch_pair(const AttnArgs& a, int64_t items, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int D, typename T, int NQW>
+hipError_t launch_decode(const AttnArgs& a, int64_t items, hipStream_t st) {
+  constexpr int lds = DecLds<D, NQW>::bytes;
+  const hipError_t attr =
+      opt_in_lds(reinterpret_cast<const void*>(&attn_decode_kernel<D, T, NQW>), lds);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((attn_decode_kernel<D, T, NQW>), dim3(unsigned(items)),
+                     dim3(64 * NQW), lds, st, a);
+  return hipGetLastError();
+}
+
 template <int D, typename T>
 hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
-  hipError_t e = p.streams == 2   ? launch_main<D, T, 2>(a, p.items, st)
-                 : p.streams == 3 ? launch_pair<D, T>(a, p.items, st)
-                                  : launch_main<D, T, 1>(a, p.items, st);
+  hipError_t e = p.kernel == kDecode
+                     ? (p.nqw == 4 ? launch_decode<D, T, 4>(a, p.items, st)
+                                   : launch_decode<D, T, 2>(a, p.items, st))
+                 : p.kernel == kDual   ? launch_main<D, T, 2>(a, p.items, st)
+                 : p.kernel == kPaired ? launch_pair<D, T>(a, p.items, st)
+                                       : launch_main<D, T, 1>(a, p.items, st);
   if (e != hipSuccess || p.comb_blocks == 0) return e;
   hipLaunchKernelGGL((attn_combine_kernel<D, T>), dim3(unsigned(p.comb_blocks)), dim3(256), 0,
                      st, a);
@@ -1905,7 +2637,13 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.cv = cache ? static_cast<const uint16_t*>(cache) + c_plane : nullptr;
   a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh;
   a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
-  a.ws_o = static_cast<uint16_t*>(workspace);
+  // Workspace: [counters (decode)][f16 partial values][fp32 records].
+  char* ws = static_cast<char*>(workspace);
+  // Counters only for the in-kernel merge: a null pointer tells the decode
+  // kernel to store plain partials for attn_combine_kernel.
+  a.counters = p.counter_bytes && p.kernel == kDecode && !p.merge_kernel
+                   ? reinterpret_cast<int32_t*>(ws) : nullptr;
+  a.ws_o = p.ws_bytes ? reinterpret_cast<uint16_t*>(ws + p.counter_bytes) : nullptr;
   a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.bm * D) : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
   a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);

@@ -61,6 +61,8 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // ---------------------------------------------------------------------------
 namespace dx {
 void set_error(const char* fmt, ...);
+// Current value of a dx_set_tuning override (0: the library's own choice).
+int tuning(int key);
 }
 
 #define DX_CHECK_ARG(cond, ...)                   \

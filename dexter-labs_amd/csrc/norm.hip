@@ -344,12 +344,8 @@ int choose_waves(int64_t C, int x_bytes) {
 }
 
 int waves_override() {
-  static const int v = [] {
-    const char* s = getenv("DX_NORM_WAVES");
-    const int n = s ? atoi(s) : 0;
-    return (n >= 1 && n <= kMaxWaves) ? n : 0;
-  }();
-  return v;
+  const int n = tuning(DX_TUNE_NORM_WAVES);
+  return n >= 1 && n <= kMaxWaves ? n : 0;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

@@ -201,11 +201,6 @@ __global__ __launch_bounds__(64 * NW) void qkv_gemm_kernel(QkvGemmArgs a) {
   }
 }
 
-long env_int(const char* name) {
-  const char* s = getenv(name);
-  return s ? atol(s) : 0;
-}
-
 template <typename T, int NW, int NM>
 hipError_t launch_nm(const QkvGemmArgs& a, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((qkv_gemm_kernel<T, NW, NM, kRing>), dim3(blocks), dim3(64 * NW), 0, st,
@@ -237,11 +232,12 @@ hipError_t launch_t(const QkvGemmArgs& a, const QkvPlan& p, hipStream_t st) {
 // closest to one workgroup per CU, fewer splits on a tie. At the Wan-5B chunk
 // that is 3 splits, 216 workgroups: measured 19.9 us for the GEMM, against
 // 26.7 us at 6 splits and 22-24 us at 2 (each a read-bandwidth and
-// partial-traffic trade). DX_QKV_WAVES (2 or 4) and DX_QKV_SPLITS override it.
+// partial-traffic trade). dx_set_tuning(DX_TUNE_QKV_WAVES / DX_TUNE_QKV_SPLITS)
+// overrides it.
 QkvPlan plan_qkv(int64_t M, int64_t C, int64_t HD) {
   QkvPlan p{};
   p.waves = 4;
-  if (env_int("DX_QKV_WAVES") == 2) p.waves = 2;
+  if (tuning(DX_TUNE_QKV_WAVES) == 2) p.waves = 2;
   const int64_t tiles = 3 * HD / (32 * p.waves);
   int s = 1;
   int64_t best = -1;
@@ -250,7 +246,7 @@ QkvPlan plan_qkv(int64_t M, int64_t C, int64_t HD) {
     const int64_t gap = tiles * c > 256 ? tiles * c - 256 : 256 - tiles * c;
     if (best < 0 || gap < best) { best = gap; s = c; }
   }
-  const long forced = env_int("DX_QKV_SPLITS");
+  const long forced = tuning(DX_TUNE_QKV_SPLITS);
   if (forced >= 1 && forced <= 16 && C % (int64_t(kStep) * forced) == 0) s = int(forced);
   p.splits = s;
   p.workspace_bytes = int64_t(s) * M * 3 * HD * int64_t(sizeof(float));

@@ -69,16 +69,20 @@ def adaln_modulate(
     shift: torch.Tensor,
     eps: float = 1e-6,
 ) -> torch.Tensor:
-    """``layer_norm(x) * (1 + scale) + shift`` in one pass.
+    """Modulated LayerNorm of the DiT block: normalise each ``C``-row of ``x`` (no
+    affine), multiply by ``1 + scale`` and add ``shift``; one kernel, one read of ``x``.
 
-    ``x`` is ``[B, L, C]``; ``scale``/``shift`` are ``[B, L, C]`` or ``[B, 1, C]``
-    (any shape that broadcasts to ``x``'s rows, ``[C]`` included).
+    ``x`` is ``[B, L, C]``. ``scale`` and ``shift`` broadcast against it: per row
+    (``[B, L, C]``), per batch (``[B, 1, C]``, the Wan block's modulation) or one
+    row for all (``[C]``). The result has torch's promoted dtype.
     """
     return select("norm", "adaln", x, scale, shift)(x, scale, shift, eps)
 
 
 def gated_residual(x: torch.Tensor, y: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
-    """``x + y * gate``, fused so the residual is read and written once."""
+    """Residual add with a gate, ``x + y * gate``: the attention or FFN branch ``y``
+    scaled by its per-channel gate and added to the stream ``x`` in one pass
+    (``gate`` broadcasts like ``adaln_modulate``'s modulation)."""
     return select("norm", "gated_residual", x, y, gate)(x, y, gate)
 
 

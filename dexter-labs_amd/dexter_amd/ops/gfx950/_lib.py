@@ -16,10 +16,13 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
+# dx_set_tuning keys (launch-schedule overrides for measurement and tests).
+(TUNE_ATTN_SPLITS, TUNE_ATTN_KERNEL, TUNE_NORM_WAVES, TUNE_QKV_SPLITS, TUNE_QKV_WAVES,
+ TUNE_ATTN_MERGE) = range(6)
 
 _DTYPE_CODE = {torch.bfloat16: DX_BF16, torch.float16: DX_F16, torch.float32: DX_F32,
                torch.int32: DX_I32, torch.int64: DX_I64}
@@ -33,6 +36,7 @@ _f = ctypes.c_float
 _SIGNATURES: dict[str, tuple[type, list]] = {
     "dx_last_error": (ctypes.c_char_p, []),
     "dx_abi_version": (_i, []),
+    "dx_set_tuning": (_i, [_i, _i]),
     "dx_qk_norm_rope": (_i, [
         _p, _l, _l, _l,            # q, strides
         _p, _l, _l, _l,            # k, strides
@@ -193,3 +197,49 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def set_tuning(key: int, value: int) -> None:
+    """Process-wide launch-schedule override (0 restores the library's choice)."""
+    check(load().dx_set_tuning(int(key), int(value)), "set_tuning")
+
+
+class tuning:
+    """Context manager for launch-schedule overrides, e.g.
+    ``with tuning(TUNE_ATTN_SPLITS, 4): ...``; restores automatic choice on exit."""
+
+    def __init__(self, key: int, value: int) -> None:
+        self.key, self.value = key, value
+
+    def __enter__(self) -> "tuning":
+        set_tuning(self.key, self.value)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        set_tuning(self.key, 0)
+
+
+_ws_lock = threading.Lock()
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """A zero-initialised scratch buffer of at least ``nbytes`` for the current stream.
+
+    One buffer per (device, stream), kept between calls and grown when needed.
+    The attention kernels keep arrival counters in it that must be zero when a
+    call starts and that every call leaves at zero, so the buffer is zeroed
+    once, when it is allocated (a fill kernel, which graph capture records).
+    Calls on one stream are ordered, so they never share it concurrently.
+    """
+    if nbytes <= 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           stream_handle(device))
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+    return buf

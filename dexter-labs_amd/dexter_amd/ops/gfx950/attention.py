@@ -127,7 +127,7 @@ def _launch(q, k, v, kv_cache, cache_len, cache_lens, block_boundaries, softmax_
     ws_bytes = lib.dx_attention_workspace_bytes(b, q_len, kv_len, heads, dim, int(cache_len), arr)
     if ws_bytes < 0:
         _lib.check(-ws_bytes, "attention workspace")
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    ws = _lib.workspace(q.device, ws_bytes)
     common = [
         q.data_ptr(), *strides(q, 3), k.data_ptr(), *strides(k, 3), v.data_ptr(), *strides(v, 3),
         cache_ptr, *c_strides, out.data_ptr(), *strides(out, 3),

@@ -129,12 +129,10 @@ class PlatformInfo:
         return all(f in self.features for f in features)
 
     def describe(self) -> str:
-        gb = self.total_memory / 1e9
-        return (
-            f"{self.device_name} [{self.arch} / {self.family}] "
-            f"{self.compute_units} CU, wave{self.wavefront}, "
-            f"{gb:.1f} GB @ {self.memory_bandwidth:.0f} GB/s"
-        )
+        """One line for error messages and ``explain``: arch first, then the device."""
+        mem = f"{self.total_memory / 2**30:.0f} GiB" if self.total_memory else "no device memory"
+        return (f"{self.arch}/{self.family} ({self.device_name}; {self.compute_units} CUs, "
+                f"{self.wavefront}-lane waves, {mem}, {self.memory_bandwidth / 1e3:.2f} TB/s)")
 
 
 @dataclass(frozen=True)
@@ -160,10 +158,9 @@ def _from_arch(arch: str, device_name: str, multiprocessors: int,
                total_memory: int) -> PlatformInfo:
     known = _AMD_ARCHS.get(arch)
     if known is None:
-        raise RuntimeError(
-            f"dexter does not know AMD architecture {arch!r}. "
-            f"Add a row to platform._AMD_ARCHS; supported: {', '.join(sorted(_AMD_ARCHS))}."
-        )
+        rows = ", ".join(sorted(_AMD_ARCHS))
+        raise RuntimeError(f"unsupported AMD architecture {arch!r}: no platform row for it "
+                           f"(rows exist for {rows})")
     return PlatformInfo(
         vendor="amd",
         arch=arch,

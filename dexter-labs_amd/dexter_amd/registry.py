@@ -1,34 +1,42 @@
 """Kernel registry: many implementations per op, one picked per call.
 
-Same contract as dexter's registry (``python/dexter/registry.py:34-173``), so
-an implementation package written against one registers into the other:
+The interface matches dexter's registry (``python/dexter/registry.py:34-152``)
+so an implementation package written against one registers into the other:
 
 * ``Priority`` bands REFERENCE=0 < PORTABLE=4 < PERFORMANT=8 < SPECIALISED=12;
-  higher wins.
-* The capability gate is checked first; a spec whose gate fails is invisible.
+  higher wins, and equal priorities keep registration order.
+* The capability gate comes first: a spec whose gate the platform fails is
+  never a candidate, whatever its priority.
 * ``DEXTER_KERNEL=<family/mode>:<name>[,...]`` pins one implementation; a pin
   naming an implementation this platform cannot run raises ``LookupError``.
-* Otherwise the first viable spec whose optional ``accepts(*args, **kwargs)``
+* Otherwise the best candidate whose optional ``accepts(*args, **kwargs)``
   predicate holds is returned; if none, ``LookupError``.
-* ``register`` rejects a duplicate name within one ``family/mode`` with
-  ``ValueError``.
+* ``register`` rejects a second spec of the same name for one ``family/mode``
+  with ``ValueError``.
 
-This package registers no torch fallback: on a platform without a HIP kernel
-for the call, selection raises instead of quietly running something else.
+Internally every decision is one pass, :func:`_rulings`, that classifies each
+registered spec for a call (gated, declined, eligible); :func:`select_spec`
+takes the first eligible one and :func:`explain` prints the whole pass. This
+package registers no torch fallback: on a platform without a HIP kernel for the
+call, selection raises instead of quietly running something else.
 """
 
 from __future__ import annotations
 
+import bisect
+import functools
+import itertools
 import os
-from collections import defaultdict
 from dataclasses import dataclass, field
 from enum import IntEnum
 from typing import Callable, Iterator
 
 from .platform import Capability, PlatformInfo, current_platform
 
-__all__ = ["Priority", "KernelSpec", "register", "select", "select_spec",
-           "candidates", "explain", "unregister"]
+__all__ = ["Priority", "KernelSpec", "register", "select", "select_spec", "candidates",
+           "explain", "registered", "unregister"]
+
+PIN_ENV = "DEXTER_KERNEL"
 
 
 class Priority(IntEnum):
@@ -42,6 +50,8 @@ class Priority(IntEnum):
 
 @dataclass(frozen=True)
 class KernelSpec:
+    """One implementation of an op, with its gate and shape predicate."""
+
     name: str
     family: str
     mode: str
@@ -52,14 +62,41 @@ class KernelSpec:
 
     @property
     def key(self) -> str:
-        return f"{self.family}/{self.mode}"
-
-    def __repr__(self) -> str:  # pragma: no cover - debugging aid
-        return f"<KernelSpec {self.key}:{self.name} pri={int(self.priority)}>"
+        return op_key(self.family, self.mode)
 
 
-# family/mode -> specs, kept sorted best-first so selection is a scan.
-_REGISTRY: dict[str, list[KernelSpec]] = defaultdict(list)
+def op_key(family: str, mode: str) -> str:
+    return f"{family}/{mode}"
+
+
+class _Catalogue:
+    """Specs per op key in selection order: priority descending, then age.
+
+    Each entry carries a sort key ``(-priority, serial)``, so inserting with
+    ``bisect`` keeps the order without re-sorting, and a spec registered later
+    at the same priority lands behind the earlier ones.
+    """
+
+    def __init__(self) -> None:
+        self._entries: dict[str, list[tuple[tuple[int, int], KernelSpec]]] = {}
+        self._serial = itertools.count()
+
+    def add(self, spec: KernelSpec) -> None:
+        entries = self._entries.setdefault(spec.key, [])
+        if any(s.name == spec.name for _, s in entries):
+            raise ValueError(f"duplicate kernel {spec.key}:{spec.name}")
+        order = (-int(spec.priority), next(self._serial))
+        bisect.insort(entries, (order, spec), key=lambda e: e[0])
+
+    def remove(self, key: str, name: str) -> None:
+        entries = self._entries.get(key, [])
+        entries[:] = [e for e in entries if e[1].name != name]
+
+    def specs(self, key: str) -> tuple[KernelSpec, ...]:
+        return tuple(s for _, s in self._entries.get(key, ()))
+
+
+_CATALOGUE = _Catalogue()
 
 
 def register(
@@ -71,66 +108,106 @@ def register(
     priority: Priority | int = Priority.PERFORMANT,
     accepts: Callable[..., bool] | None = None,
 ) -> Callable[[Callable], Callable]:
-    """Decorator: add ``fn`` as an implementation of ``family/mode``."""
+    """Decorator: add the decorated function as an implementation of ``family/mode``.
 
-    def wrap(fn: Callable) -> Callable:
-        spec = KernelSpec(name=name, family=family, mode=mode, impl=fn,
-                          capability=capability or Capability(),
-                          priority=priority, accepts=accepts)
-        bucket = _REGISTRY[spec.key]
-        if any(s.name == name for s in bucket):
-            raise ValueError(f"duplicate kernel {spec.key}:{name}")
-        bucket.append(spec)
-        bucket.sort(key=lambda s: int(s.priority), reverse=True)  # stable
+    The function comes back unchanged apart from a ``dexter_spec`` attribute
+    holding its :class:`KernelSpec`.
+    """
+    gate = capability if capability is not None else Capability()
+
+    def add(fn: Callable) -> Callable:
+        spec = KernelSpec(name, family, mode, fn, gate, priority, accepts)
+        _CATALOGUE.add(spec)
         fn.dexter_spec = spec  # type: ignore[attr-defined]
         return fn
 
-    return wrap
+    return add
 
 
 def unregister(family: str, mode: str, name: str) -> None:
     """Remove one spec (tests register throwaway specs and clean up)."""
-    bucket = _REGISTRY[f"{family}/{mode}"]
-    bucket[:] = [s for s in bucket if s.name != name]
+    _CATALOGUE.remove(op_key(family, mode), name)
+
+
+def registered(family: str, mode: str) -> tuple[KernelSpec, ...]:
+    """Every spec of ``family/mode`` in selection order, runnable here or not."""
+    return _CATALOGUE.specs(op_key(family, mode))
 
 
 def candidates(family: str, mode: str,
                platform: PlatformInfo | None = None) -> Iterator[KernelSpec]:
-    """Specs for ``family/mode`` whose gate this platform passes, best first."""
-    platform = platform or current_platform()
-    for spec in _REGISTRY[f"{family}/{mode}"]:
-        if spec.capability.satisfied_by(platform):
-            yield spec
+    """Specs of ``family/mode`` whose gate ``platform`` (default: this one) passes."""
+    where = platform if platform is not None else current_platform()
+    return (s for s in registered(family, mode) if s.capability.satisfied_by(where))
 
 
-def _pinned(key: str) -> str | None:
-    for entry in os.environ.get("DEXTER_KERNEL", "").split(","):
-        entry = entry.strip()
-        if not entry:
-            continue
-        pin_key, _, pin_name = entry.partition(":")
-        if pin_key == key:
-            return pin_name
-    return None
+@functools.lru_cache(maxsize=16)
+def _pins(raw: str) -> dict[str, str]:
+    """``DEXTER_KERNEL`` as ``{op key: pinned name}``; the first entry for a key wins.
+
+    An entry without ``:`` pins the empty name, which no spec has, so selection
+    for that op raises.
+    """
+    table: dict[str, str] = {}
+    for item in raw.split(","):
+        key, _, name = item.strip().partition(":")
+        if key:
+            table.setdefault(key, name)
+    return table
+
+
+def _pin_for(key: str) -> str | None:
+    return _pins(os.environ.get(PIN_ENV, "")).get(key)
+
+
+# Ruling of one spec for one call, in the order selection considers them.
+GATED, DECLINED, ELIGIBLE = "gated", "declined", "eligible"
+
+
+@dataclass(frozen=True)
+class Ruling:
+    spec: KernelSpec
+    status: str          # GATED, DECLINED or ELIGIBLE
+    detail: str = ""     # why a spec was gated
+
+
+def _gate_detail(spec: KernelSpec, platform: PlatformInfo) -> str:
+    missing = sorted(spec.capability.features - platform.features)
+    if missing:
+        return f"platform lacks {missing}"
+    return f"vendor/arch outside the gate ({platform.vendor} {platform.arch})"
+
+
+def _rulings(key: str, platform: PlatformInfo, args: tuple, kwargs: dict) -> list[Ruling]:
+    """Classify every spec of ``key`` for this call (predicates only for runnable specs)."""
+    out = []
+    for spec in _CATALOGUE.specs(key):
+        if not spec.capability.satisfied_by(platform):
+            out.append(Ruling(spec, GATED, _gate_detail(spec, platform)))
+        elif spec.accepts is not None and not spec.accepts(*args, **kwargs):
+            out.append(Ruling(spec, DECLINED))
+        else:
+            out.append(Ruling(spec, ELIGIBLE))
+    return out
 
 
 def select_spec(family: str, mode: str, *args, **kwargs) -> KernelSpec:
     """Like :func:`select` but returns the whole spec (name, priority, ...)."""
-    key = f"{family}/{mode}"
-    pin = _pinned(key)
-    viable = list(candidates(family, mode))
+    key = op_key(family, mode)
+    platform = current_platform()
+    pin = _pin_for(key)
     if pin is not None:
-        for spec in viable:
+        # A pin overrides the predicates, not the gate.
+        for spec in candidates(family, mode, platform):
             if spec.name == pin:
                 return spec
-        raise LookupError(f"DEXTER_KERNEL pinned {key}:{pin}, which is not available here")
-    for spec in viable:
-        if spec.accepts is None or spec.accepts(*args, **kwargs):
-            return spec
-    raise LookupError(
-        f"no kernel for {key} on {current_platform().describe()}. "
-        f"Registered: {[s.name for s in _REGISTRY[key]] or 'none'}"
-    )
+        raise LookupError(f"{PIN_ENV} pinned {key}:{pin}, which is not available here")
+    for ruling in _rulings(key, platform, args, kwargs):
+        if ruling.status == ELIGIBLE:
+            return ruling.spec
+    names = [s.name for s in _CATALOGUE.specs(key)]
+    raise LookupError(f"no kernel for {key} on {platform.describe()}. "
+                      f"Registered: {names or 'none'}")
 
 
 def select(family: str, mode: str, *args, **kwargs) -> Callable:
@@ -142,21 +219,26 @@ def select(family: str, mode: str, *args, **kwargs) -> Callable:
 
 
 def explain(family: str, mode: str, *args, **kwargs) -> str:
-    """Why each registered spec was or was not picked, one line per spec."""
-    key = f"{family}/{mode}"
+    """The selection pass for one call as text: a header, then one row per spec.
+
+    Rows are in selection order; the chosen spec is marked ``chosen``, other
+    runnable ones ``eligible``, and the rest say why they were passed over.
+    """
+    key = op_key(family, mode)
     platform = current_platform()
-    lines = [f"{key} on {platform.describe()}"]
-    chosen = None
-    for spec in _REGISTRY[key]:
-        if not spec.capability.satisfied_by(platform):
-            missing = sorted(spec.capability.features - platform.features)
-            reason = f"needs {missing}" if missing else "arch gate"
-            lines.append(f"  - {spec.name:<28} skipped ({reason})")
-        elif spec.accepts is not None and not spec.accepts(*args, **kwargs):
-            lines.append(f"  - {spec.name:<28} skipped (shape not accepted)")
-        elif chosen is None:
-            chosen = spec
-            lines.append(f"  * {spec.name:<28} SELECTED (pri={int(spec.priority)})")
-        else:
-            lines.append(f"  - {spec.name:<28} viable (pri={int(spec.priority)})")
-    return "\n".join(lines)
+    pin = _pin_for(key)
+    rows = _rulings(key, platform, args, kwargs)
+    try:
+        chosen = select_spec(family, mode, *args, **kwargs).name
+    except LookupError as err:
+        chosen, failure = None, str(err)
+    width = max((len(r.spec.name) for r in rows), default=0)
+    text = [f"{key} on {platform.describe()}" + (f" [pin: {pin}]" if pin is not None else "")]
+    for r in rows:
+        tag = "chosen" if r.spec.name == chosen and r.status != GATED else r.status
+        why = {GATED: f": {r.detail}", DECLINED: ": accepts() declined these arguments"}
+        text.append(f"  {tag:<8} {r.spec.name:<{width}}  priority {int(r.spec.priority):>2}"
+                    f"{why.get(r.status, '')}")
+    if chosen is None:
+        text.append(f"  no selection: {failure}")
+    return "\n".join(text)

@@ -1,9 +1,9 @@
 """HIP-graph capture of a control step, including the steps that write the KV cache.
 
-Mirrors ``python/dexter/runtime/graph.py``: ``GraphRunner`` replays a captured
-forward against fixed input buffers (:28-47), and ``capture`` warms up on a
-side stream before recording, so allocator and library set-up stay out of the
-graph (:50-74).
+Covers what ``python/dexter/runtime/graph.py`` offers: a runner that replays a
+recorded forward against fixed input buffers (``GraphRunner``, the interface of
+:28-47), and ``capture``, which warms the step up on a side stream before
+recording so allocator and library set-up stay out of the graph (:50-74).
 
 The reference captures only the cache-free denoising steps: the final step of
 a control step writes the KV cache at a length that grows between control
@@ -33,23 +33,35 @@ from ..models.kv_cache import KVCache
 
 
 class GraphRunner:
-    """A captured forward, replayed against fixed input buffers.
+    """A recorded step plus the tensors it reads and writes.
 
-    Callers pass ordinary tensors; they are copied into the buffers the graph
-    was captured with, so the static-address requirement stays hidden.
+    A graph reads its inputs from the addresses it was recorded with, so each
+    call copies the caller's tensors into those buffers (skipping a tensor that
+    already is the buffer), replays, and returns the graph's own output
+    tensors, which the next call overwrites. Shapes and dtypes must match the
+    recording exactly: ``copy_`` would otherwise broadcast or cast without a
+    word.
     """
+
+    __slots__ = ("graph", "inputs", "outputs")
 
     def __init__(self, graph: torch.cuda.CUDAGraph, inputs: tuple[torch.Tensor, ...],
                  outputs: tuple[torch.Tensor, ...]) -> None:
-        self.graph = graph
-        self.inputs = inputs
-        self.outputs = outputs
+        self.graph, self.inputs, self.outputs = graph, tuple(inputs), tuple(outputs)
+
+    def _stage(self, args: Sequence[torch.Tensor]) -> None:
+        if len(args) != len(self.inputs):
+            raise ValueError(f"the recorded step reads {len(self.inputs)} input tensors; "
+                             f"{len(args)} were passed")
+        for i, (buf, arg) in enumerate(zip(self.inputs, args)):
+            if arg.shape != buf.shape or arg.dtype != buf.dtype:
+                raise ValueError(f"input {i} was recorded as {tuple(buf.shape)} {buf.dtype}, "
+                                 f"got {tuple(arg.shape)} {arg.dtype}")
+            if arg.data_ptr() != buf.data_ptr():
+                buf.copy_(arg)
 
     def __call__(self, *args: torch.Tensor) -> tuple[torch.Tensor, ...]:
-        if len(args) != len(self.inputs):
-            raise ValueError(f"graph takes {len(self.inputs)} inputs, got {len(args)}")
-        for buffer, arg in zip(self.inputs, args):
-            buffer.copy_(arg)
+        self._stage(args)
         self.graph.replay()
         return self.outputs
 
@@ -58,24 +70,35 @@ def _as_tuple(out) -> tuple[torch.Tensor, ...]:
     return tuple(out) if isinstance(out, (tuple, list)) else (out,)
 
 
-def capture(fn: Callable[..., object], sample_inputs: Sequence[torch.Tensor],
-            warmup: int = 3) -> GraphRunner:
-    """Capture ``fn(*inputs)`` into a graph, after ``warmup`` eager runs on a side stream.
+def _record(fn: Callable[..., object], static: tuple[torch.Tensor, ...], warmup: int,
+            after_each_warmup: Callable[[], None] | None = None) -> GraphRunner:
+    """Run ``fn(*static)`` ``warmup`` times on a side stream (so module loads and
+    allocator growth happen outside the recording), then record one call.
 
-    ``fn`` must be shape-stable and must not synchronise with the host.
+    ``after_each_warmup`` runs after every eager call, still on the side stream.
     """
-    static = tuple(t.clone() for t in sample_inputs)
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
         for _ in range(warmup):
             fn(*static)
-    torch.cuda.current_stream().wait_stream(stream)
+            if after_each_warmup is not None:
+                after_each_warmup()
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         outputs = _as_tuple(fn(*static))
     return GraphRunner(graph, static, outputs)
+
+
+def capture(fn: Callable[..., object], sample_inputs: Sequence[torch.Tensor],
+            warmup: int = 3) -> GraphRunner:
+    """Record ``fn(*inputs)`` (shape-stable, no host synchronisation) into a graph.
+
+    The recorded inputs are copies of ``sample_inputs``.
+    """
+    return _record(fn, tuple(t.clone() for t in sample_inputs), warmup)
 
 
 class CachedStepGraph:
@@ -105,23 +128,12 @@ class CachedStepGraph:
                 c.cursor.copy_(cursor)
                 c.status.copy_(status)
 
-        static = tuple(t.clone() for t in sample_inputs)
-        stream = torch.cuda.Stream()
-        stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
-            for _ in range(warmup):
-                fn(*static)
-                restore()
-        torch.cuda.current_stream().wait_stream(stream)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            outputs = _as_tuple(fn(*static))
-        # Capture ran fn's host code once (its commits moved the host lengths)
+        self.runner = _record(fn, tuple(t.clone() for t in sample_inputs), warmup,
+                              after_each_warmup=restore)
+        # Recording ran fn's host code once (its commits moved the host lengths)
         # but no kernel: restore the host side only.
         for c, (length, _, _) in zip(self.caches, saved):
             c.length = length
-        self.runner = GraphRunner(graph, static, outputs)
 
     def __call__(self, *args: torch.Tensor) -> tuple[torch.Tensor, ...]:
         for c in self.caches:

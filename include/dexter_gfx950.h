@@ -76,7 +76,33 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 6
+#define DX_ABI_VERSION 7
+
+/*
+ * Launch-schedule overrides, for measurement and tests only: process-wide,
+ * 0 (the default) leaves the choice to the library. Results stay within the
+ * documented accuracy under every override; schedules differ in rounding.
+ * Nothing in the library reads the environment.
+ *   DX_TUNE_ATTN_SPLITS  key splits per attention work item (1..16)
+ *   DX_TUNE_ATTN_KERNEL  attention kernel: 1 single-stream, 2 dual-stream
+ *                        with a separate merge kernel, 3 paired prefill,
+ *                        4 one-launch decode
+ *   DX_TUNE_NORM_WAVES   waves per row of the adaLN / gated-residual kernels (1..16)
+ *   DX_TUNE_QKV_SPLITS   K splits of the fused QKV GEMM (1..16)
+ *   DX_TUNE_QKV_WAVES    waves per workgroup of the fused QKV GEMM (2 or 4)
+ *   DX_TUNE_ATTN_MERGE   decode split merge: 1 in the kernel, 2 by a separate
+ *                        merge kernel
+ * Returns DX_EINVAL for an unknown key or an out-of-range value.
+ * No reference counterpart (the reference's tuning is Triton's autotuner).
+ */
+#define DX_TUNE_ATTN_SPLITS 0
+#define DX_TUNE_ATTN_KERNEL 1
+#define DX_TUNE_NORM_WAVES 2
+#define DX_TUNE_QKV_SPLITS 3
+#define DX_TUNE_QKV_WAVES 4
+#define DX_TUNE_ATTN_MERGE 5
+#define DX_TUNE_KEYS 6
+int dx_set_tuning(int key, int value);
 
 /*
  * QK-RMSNorm + rotary on q and k, one token's whole H*D plane at a time.

@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import dexter_amd.ops as ops
+from dexter_amd.ops.gfx950 import _lib
 from dexter_amd.registry import select_spec
 from oracle import attention as oatt
 
@@ -162,13 +163,14 @@ def _decode_case(device, seed=50):
 
 
 @pytest.mark.parametrize("splits", [2, 3, 7, 16])
-def test_split_kv_any_split_count(device, built_lib, monkeypatch, splits):
-    """The merge of split-KV partials for 2..16 splits (16 is the maximum)
-    against the oracle, and bit-identical on a second call."""
-    monkeypatch.setenv("DX_ATTN_SPLITS", str(splits))
+def test_split_kv_any_split_count(device, built_lib, splits):
+    """The merge of split-KV partials for 2..16 splits (16 is the maximum; the
+    one-launch decode kernel takes up to 8, more go to the separate merge
+    kernel) against the oracle, and bit-identical on a second call."""
     q, k, v, cache, c = _decode_case(device)
-    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
-    again = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+    with _lib.tuning(_lib.TUNE_ATTN_SPLITS, splits):
+        got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+        again = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
     assert torch.equal(got, again)
     assert_parity(got, _oracle(q, k, v, cache, c, None), what=f"{splits} splits")
 
@@ -302,7 +304,7 @@ def test_default_scale(device, built_lib):
 
 # Prefill-shaped calls run on the paired-group kernel (two four-wave groups
 # half a tile apart, three LDS stages, its loops unrolled over the stages);
-# DX_ATTN_STREAMS=1 forces the plain single-stream schedule, whose arithmetic
+# the single-stream kernel (TUNE_ATTN_KERNEL 1) is the plain schedule, whose arithmetic
 # is the same in the same order (with one split, so no partials are rounded;
 # tiles a 256-row item visits past a 128-row item's range are fully masked
 # for the earlier rows and add exact zeros). Tile counts 1..7 per work item cover every
@@ -322,8 +324,7 @@ def test_default_scale(device, built_lib):
     (64, torch.bfloat16, 300, 0, [0, 96, 160]),
     (64, torch.float16, 192, 100, None),
 ])
-def test_prefill_schedules_agree_bit_exact(device, built_lib, monkeypatch, d, dtype, q_len,
-                                           cache_len, blocks):
+def test_prefill_schedules_agree_bit_exact(device, built_lib, d, dtype, q_len, cache_len, blocks):
     h = 4
     q = _rand((1, q_len, h, d), device, dtype=dtype, scale=0.5, seed=71)
     k = _rand((1, q_len, h, d), device, dtype=dtype, seed=72)
@@ -332,12 +333,11 @@ def test_prefill_schedules_agree_bit_exact(device, built_lib, monkeypatch, d, dt
              if cache_len else None)
     bb = torch.tensor(blocks, device=device) if blocks else None
 
-    monkeypatch.setenv("DX_ATTN_SPLITS", "1")  # whole key ranges: no partials to round
-
-    def run(streams):
-        monkeypatch.setenv("DX_ATTN_STREAMS", str(streams))
-        return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
-                                              block_boundaries=bb)
+    def run(kernel):
+        # One split (whole key ranges: no partials to round), kernel forced.
+        with _lib.tuning(_lib.TUNE_ATTN_SPLITS, 1), _lib.tuning(_lib.TUNE_ATTN_KERNEL, kernel):
+            return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
+                                                  block_boundaries=bb)
 
     paired, single = run(3), run(1)
     torch.cuda.synchronize()

@@ -8,6 +8,7 @@ and platform gates (``python/dexter/platform.py:169-185``), using fake
 from __future__ import annotations
 
 import dataclasses
+import re
 
 import pytest
 import torch
@@ -54,7 +55,7 @@ def test_cdna4_platform_row():
 
 
 def test_unknown_amd_arch_raises():
-    with pytest.raises(RuntimeError, match="does not know AMD architecture 'gfx1234'"):
+    with pytest.raises(RuntimeError, match="unsupported AMD architecture 'gfx1234'"):
         plat._from_arch("gfx1234", "x", 1, 0)
 
 
@@ -77,7 +78,7 @@ def test_gates_do_not_cross():
     ("norm/gated_residual", "hip_gated_residual_gfx950"),
 ])
 def test_hip_kernels_registered_specialised(key, name):
-    specs = reg._REGISTRY[key]
+    specs = reg.registered(*key.split("/"))
     spec = next(s for s in specs if s.name == name)
     assert int(spec.priority) == int(reg.Priority.SPECIALISED)
     assert spec.capability == CDNA4
@@ -90,7 +91,7 @@ def test_selection_on_cdna4_picks_hip(cdna4):
     q = torch.zeros(1, 4, 2, 64, dtype=torch.bfloat16)  # CPU tensor: declined by accepts
     text = reg.explain(fam, mode, q, q, q)
     assert "gfx950" in text and "hip_blockwise_causal_gfx950" in text
-    assert "shape not accepted" in text
+    assert "declined" in text and "no selection" in text
 
 
 def test_no_fallback_on_cpu(cpu):
@@ -122,7 +123,7 @@ def test_accepts_declines_shapes_the_kernel_does_not_cover(cdna4):
 def scratch_family():
     fam, mode = "test", "probe"
     yield fam, mode
-    for s in list(reg._REGISTRY[f"{fam}/{mode}"]):
+    for s in reg.registered(fam, mode):
         reg.unregister(fam, mode, s.name)
 
 
@@ -161,7 +162,8 @@ def test_accepts_predicate_and_args_not_forwarded(cdna4, scratch_family):
     assert reg.select(fam, mode, 3)() == "small"
     assert reg.select(fam, mode, 30)() == "any"
     assert seen == [3, 30]
-    assert "shape not accepted" in reg.explain(fam, mode, 30)
+    text = reg.explain(fam, mode, 30)
+    assert re.search(r"declined +small", text) and re.search(r"chosen +any", text)
 
 
 def test_pin_wins_and_bad_pin_raises(cdna4, scratch_family, monkeypatch):
@@ -193,3 +195,48 @@ def test_platform_info_is_frozen():
     p = plat.cdna4_platform()
     with pytest.raises(dataclasses.FrozenInstanceError):
         p.arch = "x"  # type: ignore[misc]
+
+
+def test_equal_priority_keeps_registration_order(cdna4, scratch_family):
+    fam, mode = scratch_family
+    for name in ("first", "second", "third"):
+        reg.register(fam, mode, name=name, priority=8)(lambda n=name: n)
+    reg.register(fam, mode, name="top", priority=12, accepts=lambda: False)(lambda: "top")
+    assert [s.name for s in reg.registered(fam, mode)] == ["top", "first", "second", "third"]
+    assert reg.select(fam, mode)() == "first"
+    reg.unregister(fam, mode, "first")
+    assert reg.select(fam, mode)() == "second"
+
+
+def test_pin_overrides_accepts_but_not_gate(cdna4, scratch_family, monkeypatch):
+    fam, mode = scratch_family
+    reg.register(fam, mode, name="picky", priority=12, accepts=lambda: False)(lambda: "picky")
+    reg.register(fam, mode, name="gated", priority=12,
+                 capability=plat.Capability(vendors=frozenset({"nvidia"})))(lambda: "gated")
+    monkeypatch.setenv("DEXTER_KERNEL", f"{fam}/{mode}:picky")
+    assert reg.select(fam, mode)() == "picky"
+    monkeypatch.setenv("DEXTER_KERNEL", f"{fam}/{mode}:gated")
+    with pytest.raises(LookupError, match="not available here"):
+        reg.select(fam, mode)
+    # An entry without ':' pins the empty name: nothing matches.
+    monkeypatch.setenv("DEXTER_KERNEL", f"{fam}/{mode}")
+    with pytest.raises(LookupError, match=f"pinned {fam}/{mode}:,"):
+        reg.select(fam, mode)
+    # The first entry for a key wins.
+    monkeypatch.setenv("DEXTER_KERNEL", f"{fam}/{mode}:picky,{fam}/{mode}:gated")
+    assert reg.select(fam, mode)() == "picky"
+
+
+def test_explain_rows(cdna4, scratch_family):
+    fam, mode = scratch_family
+    reg.register(fam, mode, name="wmma", priority=12,
+                 capability=plat.Capability(features=frozenset({"mma:wmma"})))(lambda: 0)
+    reg.register(fam, mode, name="small", priority=8, accepts=lambda x: x < 10)(lambda: 1)
+    reg.register(fam, mode, name="any", priority=4)(lambda: 2)
+    rows = reg.explain(fam, mode, 30).splitlines()
+    assert rows[0].startswith(f"{fam}/{mode} on ") and "gfx950" in rows[0]
+    assert re.match(r"  gated +wmma +priority 12: platform lacks \['mma:wmma'\]", rows[1])
+    assert re.match(r"  declined +small +priority  8: accepts\(\) declined", rows[2])
+    assert re.match(r"  chosen +any +priority  4$", rows[3])
+    rows = reg.explain(fam, mode, 3).splitlines()
+    assert re.match(r"  chosen +small", rows[2]) and re.match(r"  eligible +any", rows[3])
