@@ -2070,24 +2070,27 @@ __global__ __launch_bounds__(64 * NQW, 1) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
     if (!sh[2]) continue;
     const int r_lo = c * nrows / S, rn = (c + 1) * nrows / S - r_lo;
+    // Every load is issued before any is used, with no branch between them
+    // (a guarded load compiles to a wait on every earlier one): splits
+    // sp >= S read past the descriptors' bound and return zeros, and rows
+    // r >= rn re-read the chunk's last row; both go unused.
     f32x4 rv[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      const int idx = int(threadIdx.x) + NT * i, sp = idx / (kRows / 2), r = idx % (kRows / 2);
-      if (sp < S && r < rn)
-        rv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rrec, (uint32_t(sp) * ws_rows + r_lo + r) * 16, 0, kSc1));
+      const int idx = int(threadIdx.x) + NT * i, sp = idx / (kRows / 2);
+      const int r = min(idx % (kRows / 2), rn - 1);
+      rv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rrec, (uint32_t(sp) * ws_rows + r_lo + r) * 16, 0, kSc1));
     }
     u32x4 val[UPT][kMaxDecSplits];
 #pragma unroll
     for (int k = 0; k < UPT; ++k) {
-      const int u = int(threadIdx.x) + NT * k, r = u / CR, ch = u % CR;
+      const int u = int(threadIdx.x) + NT * k, r = min(u / CR, rn - 1), ch = u % CR;
 #pragma unroll
       for (int sp = 0; sp < kMaxDecSplits; ++sp)
-        if (sp < S && r < rn)
-          val[k][sp] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                         rws, ((uint32_t(sp) * ws_rows + r_lo + r) * D + ch * 8) * 2, 0, kSc1));
+        val[k][sp] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rws, ((uint32_t(sp) * ws_rows + r_lo + r) * D + ch * 8) * 2, 0, kSc1));
     }
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -2169,43 +2172,45 @@ template <int D> struct CombineShape {
 template <int NMAX>
 __device__ __forceinline__ f32x4 merge_partials(const f32x4 (&ml)[NMAX], const u32x2 (&o)[NMAX],
                                                 int n) {
+  // Splits s >= n hold zeros (loads past the buffer bound) and are masked
+  // by selects, not branches, so every load is issued before any is used.
   float mmax = -INFINITY;
   int emax = INT_MIN;
 #pragma unroll
-  for (int s = 0; s < NMAX; ++s)
-    if (s < n) {
-      mmax = fmaxf(mmax, ml[s][0]);
-      emax = max(emax, int(ml[s][2]));
-    }
+  for (int s = 0; s < NMAX; ++s) {
+    mmax = s < n ? fmaxf(mmax, ml[s][0]) : mmax;
+    emax = s < n ? max(emax, int(ml[s][2])) : emax;
+  }
   const float base = mmax == -INFINITY ? 0.f : mmax;
   float w[NMAX];
   float L = 0.f;
 #pragma unroll
-  for (int s = 0; s < NMAX; ++s)
-    if (s < n) {
-      w[s] = fast_exp2(ml[s][0] - base) * ml[s][1];
-      L += w[s];
-    }
+  for (int s = 0; s < NMAX; ++s) {
+    w[s] = s < n ? fast_exp2(ml[s][0] - base) * ml[s][1] : 0.f;
+    L += w[s];
+  }
   const float invL = 1.0f / L;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < NMAX; ++s)
-    if (s < n) {
-      const float c = __builtin_ldexpf(w[s] * invL, int(ml[s][2]) - emax);
-      acc[0] += c * to_f32(f16_t{uint16_t(o[s][0] & 0xffffu)});
-      acc[1] += c * to_f32(f16_t{uint16_t(o[s][0] >> 16)});
-      acc[2] += c * to_f32(f16_t{uint16_t(o[s][1] & 0xffffu)});
-      acc[3] += c * to_f32(f16_t{uint16_t(o[s][1] >> 16)});
-    }
+  for (int s = 0; s < NMAX; ++s) {
+    const float c = s < n ? __builtin_ldexpf(w[s] * invL, int(ml[s][2]) - emax) : 0.f;
+    acc[0] += c * to_f32(f16_t{uint16_t(o[s][0] & 0xffffu)});
+    acc[1] += c * to_f32(f16_t{uint16_t(o[s][0] >> 16)});
+    acc[2] += c * to_f32(f16_t{uint16_t(o[s][1] & 0xffffu)});
+    acc[3] += c * to_f32(f16_t{uint16_t(o[s][1] >> 16)});
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) acc[e] = __builtin_ldexpf(acc[e], emax);
   return acc;
 }
 
 // Merge split-KV partials (merge_partials). Each thread owns 4 consecutive
-// dims of a row and issues every load it needs before combining. Blocks of
+// dims of a row and issues all NMAX (>= the group's split count) record and
+// value loads before combining: buffer descriptors bounded by the group's
+// n_splits partials return zeros for the rest, with no branch between the
+// loads (a guarded load compiles to a wait on every earlier one). Blocks of
 // one (batch, head) run on the XCD whose L2 holds that head's partials.
-template <int D, typename T>
+template <int D, typename T, int NMAX>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   prefetch_args(a);
   using CS = CombineShape<D>;
@@ -2216,14 +2221,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int dim = 4 * (threadIdx.x % CS::TPR);
   const int qi = cd.qtile * a.bm + row;
   if (row >= a.bm || qi >= a.Lq) return;
-  f32x4 ml[kMaxSplits];
-  u32x2 o[kMaxSplits];
+  const uint32_t rows = uint32_t(a.bm), n = uint32_t(cd.n_splits);
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + cd.pbase * a.bm * 4, (short)0, int(n * rows * 16), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rval = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o + cd.pbase * a.bm * D, (short)0, int(n * rows * D * 2), kBufWord3);
+  f32x4 ml[NMAX];
+  u32x2 o[NMAX];
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
-    if (s < cd.n_splits) {
-      ml[s] = *reinterpret_cast<const f32x4*>(a.ws_ml + ((cd.pbase + s) * a.bm + row) * 4);
-      o[s] = *reinterpret_cast<const u32x2*>(a.ws_o + ((cd.pbase + s) * a.bm + row) * D + dim);
-    }
+  for (int s = 0; s < NMAX; ++s) {
+    const uint32_t r = uint32_t(s) * rows + uint32_t(row);
+    ml[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rrec, r * 16, 0, 0));
+    o[s] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                         rval, (r * D + uint32_t(dim)) * 2, 0, 0));
   }
   const f32x4 acc = merge_partials(ml, o, cd.n_splits);
   uint16_t* op = a.out + cd.b * a.o_sb + int64_t(qi) * a.o_sl + cd.h * a.o_sh + dim;
@@ -2552,8 +2562,12 @@ hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
                  : p.kernel == kPaired ? launch_pair<D, T>(a, p.items, st)
                                        : launch_main<D, T, 1>(a, p.items, st);
   if (e != hipSuccess || p.comb_blocks == 0) return e;
-  hipLaunchKernelGGL((attn_combine_kernel<D, T>), dim3(unsigned(p.comb_blocks)), dim3(256), 0,
-                     st, a);
+  int most = p.uniform_splits;
+  for (int sk : p.seg_splits) most = std::max(most, sk);
+  const dim3 grid(unsigned(p.comb_blocks));
+  if (most <= 4) hipLaunchKernelGGL((attn_combine_kernel<D, T, 4>), grid, dim3(256), 0, st, a);
+  else if (most <= 8) hipLaunchKernelGGL((attn_combine_kernel<D, T, 8>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((attn_combine_kernel<D, T, kMaxSplits>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -47,3 +47,39 @@ def assert_parity_scaled(got, ref, max_rel=MAX_ABS, mean_abs=MEAN_ABS, what=""):
         f"{what}: max-abs {d.max().item():.3e} at scaled {scaled:.3e} (<= {max_rel}), "
         f"mean-abs {d.mean().item():.3e} (<= {mean_abs}), max |ref| {r.abs().max().item():.1f}")
     return d.max().item(), d.mean().item()
+
+
+def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at each entry of the bf16 tensor ``x`` (fp32).
+
+    |x| in [2^(e-1), 2^e) has spacing 2^(e-8) (8 significant bits); zeros and
+    subnormals take the subnormal spacing 2^-133.
+    """
+    _, e = torch.frexp(x.float())
+    return torch.where(x.float().abs() >= 2.0 ** -126, torch.ldexp(torch.ones_like(x, dtype=torch.float32), e - 8),
+                       torch.full_like(x, 2.0 ** -133, dtype=torch.float32))
+
+
+def assert_within_ulp(got, ref, ulps=1, frac=0.999, min_abs=1.0, mean_abs=MEAN_ABS, what=""):
+    """Strict parity for a bf16 kernel where ``assert_parity_scaled`` relaxes
+    the absolute bar (|ref| >= ``min_abs``, 1 by default): against the fp32
+    reference rounded to bf16, at least ``frac`` of those elements are within
+    ``ulps`` bf16 spacings. The mean-abs error over all elements stays <=
+    ``mean_abs``. Elements below ``min_abs`` keep the absolute bar: near zero
+    a spacing-based bound is meaningless, since the error of a sum of
+    probability-weighted values scales with the terms, not with the sum.
+    """
+    g = got.detach().cpu()
+    assert g.dtype == torch.bfloat16, f"{what}: expected a bf16 output"
+    assert torch.isfinite(g.float()).all(), f"{what}: non-finite output"
+    r = ref.detach().float().cpu()
+    r16 = r.to(torch.bfloat16)
+    n_ulp = (g.float() - r16.float()).abs() / bf16_ulp(r16)
+    sel = r16.float().abs() >= min_abs
+    within = (n_ulp[sel] <= ulps).float().mean().item() if sel.any() else 1.0
+    mn = (g.float() - r).abs().mean().item()
+    assert within >= frac and mn <= mean_abs, (
+        f"{what}: {within:.5f} of {int(sel.sum())} elements with |ref| >= {min_abs} within "
+        f"{ulps} bf16 ulp (>= {frac}), max {n_ulp[sel].max().item():.1f} ulp there, "
+        f"mean-abs {mn:.3e} (<= {mean_abs})")
+    return within
