@@ -2573,6 +2573,58 @@ hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Static scratch of the no-allocation entry point: one copy per device,
+// holding the layout a caller's workspace does ([counters][partial values]
+// [records]). Device globals are zero when the code object loads, and every
+// completed decode launch leaves its counters zero again; the first call on
+// a device also clears the counter region (a fill kernel on the caller's
+// stream, never a memset: the call may be under graph capture).
+constexpr int64_t kScratchBytes = DX_ATTN_SCRATCH_BYTES;
+static_assert(kScratchBytes > kCounterRegion, "scratch holds the counter region");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(u32x4* p, int64_t n) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += int64_t(gridDim.x) * 256)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// Device address of `scratch` on the current device: hipGetSymbolAddress,
+// with that device current, once per device. In host code the array's name
+// is a host-side stand-in and never a device address, so only this pointer
+// reaches kernels.
+int scratch_on_device(void** out, hipStream_t st) {
+  static std::mutex mu;
+  static std::vector<void*> addr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("attention (no-alloc): hipGetDevice failed: %s", hipGetErrorString(e));
+    return DX_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (int(addr.size()) <= dev) addr.resize(dev + 1, nullptr);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("attention (no-alloc): hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return DX_ELAUNCH;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st, static_cast<u32x4*>(p),
+                       kCounterRegion / 16);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_error("attention (no-alloc): clearing the scratch counters failed: %s",
+                hipGetErrorString(e));
+      return DX_ELAUNCH;
+    }
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return DX_OK;
+}
+
 int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k,
                     int64_t k_sb, int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb,
                     int64_t v_sl, int64_t v_sh, const void* cache, int64_t c_plane,
@@ -2581,7 +2633,8 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                     int64_t H, int64_t Hkv, int64_t D, int64_t cache_len,
                     const int64_t* cache_lens, const int32_t* cache_len_dev,
                     const void* starts, int starts_dtype, int64_t n_blocks, int causal,
-                    float softmax_scale, void* workspace, int64_t ws_bytes, void* stream) {
+                    float softmax_scale, void* workspace, int64_t ws_bytes, void* stream,
+                    bool from_scratch = false) {
   DX_CHECK_ARG(dtype == DX_BF16 || dtype == DX_F16,
                "attention: dtype code %d unsupported (bf16 or f16)", dtype);
   DX_CHECK_ARG(D == 64 || D == 128, "attention: head_dim %lld unsupported (64 or 128)",
@@ -2635,6 +2688,17 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   if (B * Lq == 0) return DX_OK;
   const Plan p = make_plan(B, Lq, Lk, H, D, cache_len, cache_lens);
   DX_CHECK_ARG(p.items < (int64_t(1) << 31), "attention: grid too large");
+  if (p.ws_bytes > 0 && from_scratch) {
+    if (p.ws_bytes > kScratchBytes) {
+      set_error("attention (no-alloc): this call needs %lld bytes of workspace, more than the "
+                "%lld-byte static scratch; use dx_blockwise_causal_attention with a workspace",
+                (long long)p.ws_bytes, (long long)kScratchBytes);
+      return DX_EWORKSPACE;
+    }
+    const int rc = scratch_on_device(&workspace, static_cast<hipStream_t>(stream));
+    if (rc != DX_OK) return rc;
+    ws_bytes = kScratchBytes;
+  }
   if (p.ws_bytes > 0) {
     if (!workspace || ws_bytes < p.ws_bytes) {
       set_error("attention: workspace of %lld bytes needed, %lld given",
@@ -2717,6 +2781,20 @@ extern "C" int dx_blockwise_causal_attention(
                          c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
                          Hkv, D, cache_len, nullptr, nullptr, block_starts, starts_dtype,
                          n_blocks, causal, softmax_scale, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dx_blockwise_causal_attention_noalloc(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k, int64_t k_sb,
+    int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh, void* out,
+    int64_t o_sb, int64_t o_sl, int64_t o_sh, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+    int64_t H, int64_t Hkv, int64_t D, int64_t cache_len, const void* block_starts,
+    int starts_dtype, int64_t n_blocks, int causal, float softmax_scale, void* stream) {
+  return attention_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, cache,
+                         c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, dtype, B, Lq, Lk, H,
+                         Hkv, D, cache_len, nullptr, nullptr, block_starts, starts_dtype,
+                         n_blocks, causal, softmax_scale, nullptr, 0, stream,
+                         /*from_scratch=*/true);
 }
 
 extern "C" int dx_blockwise_causal_attention_dev(

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -73,6 +73,16 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         _l, _p, _i, _l,            # cache_len, starts, starts dtype, n_blocks
         _i, _f,                    # causal, scale
         _p, _l, _p]),              # workspace, bytes, stream
+    "dx_blockwise_causal_attention_noalloc": (_i, [
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l,
+        _p, _l, _l, _l, _l,
+        _p, _l, _l, _l,
+        _i, _l, _l, _l, _l, _l, _l,
+        _l, _p, _i, _l,
+        _i, _f,
+        _p]),                      # stream (no workspace)
     "dx_blockwise_causal_attention_varlen": (_i, [
         _p, _l, _l, _l,
         _p, _l, _l, _l,

@@ -76,7 +76,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 7
+#define DX_ABI_VERSION 8
 
 /*
  * Launch-schedule overrides, for measurement and tests only: process-wide,
@@ -182,7 +182,11 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  * D: 64 or 128.
  * out may be strided like q. cache may be NULL when cache_len == 0.
  * workspace must hold dx_attention_workspace_bytes(...) bytes for the same
- * shape (it may be NULL when that is 0); its contents need no initialisation.
+ * shape (it may be NULL when that is 0). Its first 256 KiB hold the
+ * one-launch decode kernel's arrival counters (DX_TUNE_ATTN_KERNEL 4 with
+ * the in-kernel merge): they must be zero before a workspace is first used,
+ * and every completed call leaves them zero. The rest needs no
+ * initialisation. Calls that share a workspace must not overlap.
  * Replaces: ops/gfx1151/attention/blockwise_causal.py:146-173.
  */
 int dx_blockwise_causal_attention(
@@ -195,6 +199,30 @@ int dx_blockwise_causal_attention(
     int64_t cache_len, const void* block_starts, int starts_dtype, int64_t n_blocks,
     int causal, float softmax_scale,
     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * As dx_blockwise_causal_attention, allocating nothing: the workspace is a
+ * static per-device scratch of DX_ATTN_SCRATCH_BYTES (64 MiB) in the
+ * library, held by each device the library runs on until the process ends.
+ * A call whose dx_attention_workspace_bytes(...) exceeds it fails with
+ * DX_EWORKSPACE before any launch. The call makes no hipMalloc/hipFree; the
+ * first call on a device also launches a small kernel that clears the
+ * scratch's counter region. Every call on a device shares that device's
+ * scratch, so calls that overlap on one device (concurrent streams) race.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+#define DX_ATTN_SCRATCH_BYTES (64ll << 20)
+int dx_blockwise_causal_attention_noalloc(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+    const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    const void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+    void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+    int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t Hkv, int64_t D,
+    int64_t cache_len, const void* block_starts, int starts_dtype, int64_t n_blocks,
+    int causal, float softmax_scale, void* stream);
 
 /*
  * As dx_blockwise_causal_attention, with cache_lens[b] (a host array of B

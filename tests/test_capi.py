@@ -119,3 +119,23 @@ def test_norm_entry_points_validate_before_any_launch(built_lib):
     assert rc == _lib.DX_EINVAL and "grid limits" in lib.dx_last_error().decode()
     with pytest.raises(ValueError, match="grid limits"):
         _lib.check(rc, "gated_residual")
+
+
+def test_noalloc_refuses_a_call_beyond_its_scratch_before_any_launch(built_lib):
+    """The no-allocation entry point plans first and refuses a call whose
+    workspace exceeds the static scratch (64 MiB) without touching memory:
+    128 heads x 16 forced splits need ~71 MB of partials."""
+    lib = _lib.load()
+    h, d, lq, c = 128, 128, 128, 4096
+    row = h * d  # [B, L, H, D] contiguous: strides (L*H*D, H*D, D)
+    qkv = [16, lq * row, row, d] * 3
+    cache = [16, (c + lq) * row, (c + lq) * row, row, d]
+    out = [16, lq * row, row, d]
+    with _lib.tuning(_lib.TUNE_ATTN_SPLITS, 16):
+        need = lib.dx_attention_workspace_bytes(1, lq, lq, h, d, c, None)
+        rc = lib.dx_blockwise_causal_attention_noalloc(
+            *qkv, *cache, *out, _lib.DX_BF16, 1, lq, lq, h, h, d, c, None, _lib.DX_I32, 0, 0,
+            0.088, None)
+    assert need > (64 << 20)
+    assert rc == _lib.DX_EWORKSPACE
+    assert "static scratch" in lib.dx_last_error().decode()
