@@ -104,10 +104,13 @@ struct AttnArgs {
   // (cache_len then holds the cache capacity the launch was planned for), so
   // a captured graph follows the cache as it grows between replays.
   const int32_t* cache_len_dev;
-  // Single-launch decode: one arrival counter per work-item group (indexed by
-  // the group's first partial, 32 ints apart), zero before the launch and
-  // returned to zero by the group's last workgroup.
+  // Single-launch decode: the merge state of each work-item group
+  // (kCounterStride ints, indexed by the group's first partial), zero before
+  // the launch and returned to zero by the group's workgroups.
   int32_t* counters;
+  // Time a workgroup waits for its group on the L2 fast path of the
+  // in-kernel merge (s_memrealtime ticks); 0 skips the fast path.
+  uint32_t fast_ticks;
   int seg_b[kMaxSeg], seg_splits[kMaxSeg], seg_cache[kMaxSeg];
   int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
 };
@@ -1644,25 +1647,25 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 // Decode-shaped calls: split-KV in one launch.
 //
 // A work item is (batch, head, query group, key split). Its workgroup has NQW
-// waves, each owning 32 queries of the group (up to 32 NQW rows), and all of
-// them read every key tile of the split. On MI355X a CU takes in about
-// 50 GB/s whether the bytes come from HBM, L2 or LDS DMA, and the chip moves
-// bytes into CUs at about the HBM rate whatever their source, so every K/V
-// byte should reach exactly one CU: the planner keeps one query group where
-// it can and picks the splits from a cost model.
+// compute waves, each owning 32 queries of the group (up to 32 NQW rows), and
+// one producer wave; all compute waves read every key tile of the split. On
+// MI355X a CU takes in about 50 GB/s whether the bytes come from HBM, L2 or
+// LDS DMA, and the chip moves bytes into CUs at about the HBM rate whatever
+// their source, so every K/V byte should reach exactly one CU: the planner
+// keeps one query group where it can and picks the splits from a cost model.
 //
-// Loads. A wave issues LDS DMA for its own Q rows, then its share of the
-// split's first kDecSlots K/V tiles (the swizzled unpadded layout of the
-// prefill kernel); a slot is refilled once every wave is done with its tile.
-// Memory instructions stall at issue once enough are in flight, so nothing
-// else is put between the first loads and the wait for them.
-//
-// No workgroup barrier in the tile loop: each wave waits for its own pieces
-// of a tile (a compile-time vmcnt: every wave issues the same count per
-// tile, dead tiles reading past their buffer), then counts itself in on the
-// slot's arrival counter in LDS and waits there for the other waves, so a
-// tile is computed as soon as its bytes have landed while later tiles stream
-// in.
+// Loads. Memory instructions stall at issue once enough are in flight (a CU
+// takes a 1 KB piece about every 20 ns), and a wave stalled at issue runs
+// nothing else. So the compute waves issue no loads: the producer wave issues
+// the LDS DMA of the group's Q rows and of the K/V tiles (the swizzled
+// unpadded layout of the prefill kernel), two tiles ahead, into three slots
+// (tile j in slot j % 3). It waits for tile j's pieces with its own vmcnt,
+// then publishes the tile in LDS (the slot's generation, j / 3 + 1); before
+// refilling a slot it waits until every compute wave's count of tiles done
+// has passed the slot's previous tile. No workgroup barrier in the tile loop:
+// a compute wave waits for a tile's generation, computes it and records it
+// done, so a tile is computed as soon as its bytes have landed while later
+// tiles stream in.
 //
 // Merge. Each split stores its partial (partial_scale format), then either a
 // separate merge kernel combines them (attn_combine_kernel), or the splits
@@ -1681,118 +1684,122 @@ constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4; 
 // s_memrealtime ticks (100 MHz), 50 us. Reached only when a split cannot be
 // scheduled; the last arrival then merges the waiting workgroup's rows.
 constexpr uint64_t kSpinTicks = 5000;
-static_assert(2 + kMaxDecSplits <= kCounterStride, "group state fits its slot");
+// Wait of the L2 fast path for the group's other splits: 20 us, ample for
+// co-resident workgroups (they arrive within a few us of each other).
+constexpr uint32_t kFastTicks = 2000;
+static_assert(4 + 2 + kMaxDecSplits <= kCounterStride, "group state fits its slot");
 
-// K/V tile slots in LDS: four, or three where four tiles and the Q rows
-// would not fit (head_dim 128 with four query waves).
-template <int D, int NQW> struct DecSlots {
-  static constexpr int value = D == 128 && NQW == 4 ? 3 : 4;
-};
+// K/V tile slots in LDS (tile j of a work item in slot j % kDecSlots).
+constexpr int kDecSlots = 3;
 
 template <int D, int NQW> struct DecLds {
-  static constexpr int SL = DecSlots<D, NQW>::value;
-  using L = PairLds<D, SL>;
-  static constexpr int q_off = L::bytes;      // Q rows, K-swizzled (wave w: rows 32 w..)
-  static constexpr int sync_off = q_off + 32 * NQW * D * 2;  // slot counters, merge flags
-  static constexpr int bytes = sync_off + 2 * SL * 4 + 16;
+  using L = PairLds<D, kDecSlots>;
+  static constexpr int q_off = L::bytes;                     // Q rows, K-swizzled (wave w: rows 32 w..)
+  static constexpr int sync_off = q_off + 32 * NQW * D * 2;  // slot generations, tiles done per wave, merge flags
+  static constexpr int bytes = sync_off + 64;
   static_assert(bytes <= 160 * 1024, "decode LDS must fit one workgroup");
 };
 
-// The decode kernel's DMA: piece p of a K (or V) tile goes to wave p % NQW,
-// and each wave fetches its own 32 Q rows (loaded through LDS, not into
-// registers directly: the compiler cannot count the inline-assembly pieces,
-// so its own wait for a register load issued before them would wait for
-// them all). Lane l of a piece fills physical chunk l % CR of row l / CR and
+// The producer wave's DMA: all PK pieces of a K tile, then of its V tile
+// (piece p: rows [p RPP, (p + 1) RPP)), and the NQ pieces of the group's Q
+// rows. Lane l of a piece fills physical chunk l % CR of row l / CR and
 // fetches the logical chunk the swizzle puts there.
 template <int D, int NQW>
 struct DecDma {
-  static constexpr int SL = DecSlots<D, NQW>::value;
-  using L = PairLds<D, SL>;
+  using L = PairLds<D, kDecSlots>;
   static constexpr int CR = D / 8;                // 16-byte chunks per row
   static constexpr int RPP = 64 / CR;             // rows per piece
   static constexpr int PK = kBN / RPP;            // pieces per K (or V) tile
-  static constexpr int NK = PK / NQW;             // K (and V) pieces per wave and tile
-  static constexpr int NQ = 32 / RPP;             // Q pieces per wave (its 32 rows)
-  static constexpr int per_tile = 2 * NK;         // a wave's pieces per tile
-  static_assert(PK % NQW == 0, "even piece deal");
-  uint32_t on[2 * NK], dc[2 * NK];  // lane offset in its tile (new-key stride), cache-stride delta
-  uint32_t qo[NQ];                  // lane offset of its Q pieces
+  static constexpr int NQ = 32 * NQW / RPP;       // Q pieces of the group
+  static constexpr int per_tile = 2 * PK;         // pieces per tile
+  static_assert(per_tile <= 63, "a tile's pieces fit the vmcnt counter");
+  uint32_t on[per_tile], dc[per_tile];  // lane offset in its tile (new-key stride), cache-stride delta
+  uint32_t qo[NQ];                      // lane offset of each Q piece
 
-  __device__ __forceinline__ void init(int wid, int lane, const KvSrc& src, int q_sl2) {
+  __device__ __forceinline__ void init(int lane, const KvSrc& src, int q_sl2) {
 #pragma unroll
-    for (int m = 0; m < 2 * NK; ++m) {
-      const int r = (wid + NQW * (m % NK)) * RPP + lane / CR, x = lane % CR;
-      const int c = m < NK ? x ^ L::kswz(r) : x ^ (4 * L::vswz(r));
-      const uint32_t sn = uint32_t(m < NK ? src.k_sl2 : src.v_sl2);
+    for (int m = 0; m < per_tile; ++m) {
+      const int r = (m % PK) * RPP + lane / CR, x = lane % CR;
+      const int c = m < PK ? x ^ L::kswz(r) : x ^ (4 * L::vswz(r));
+      const uint32_t sn = uint32_t(m < PK ? src.k_sl2 : src.v_sl2);
       on[m] = uint32_t(r) * sn + uint32_t(c * 16);
       dc[m] = uint32_t(r) * (uint32_t(src.c_ss2) - sn);
     }
 #pragma unroll
     for (int m = 0; m < NQ; ++m) {
-      const int r = wid * 32 + m * RPP + lane / CR, x = lane % CR;
+      const int r = m * RPP + lane / CR, x = lane % CR;
       qo[m] = uint32_t(r) * uint32_t(q_sl2) + uint32_t((x ^ L::kswz(r)) * 16);
     }
   }
-  // This wave's Q rows of the query group into the Q area.
-  __device__ __forceinline__ void issue_q(__amdgpu_buffer_rsrc_t rq, uint32_t lds_b, int wid) const {
+  // The group's Q rows into the Q area.
+  __device__ __forceinline__ void issue_q(__amdgpu_buffer_rsrc_t rq, uint32_t lds_b) const {
 #pragma unroll
-    for (int m = 0; m < NQ; ++m)
-      dma_piece_at(rq, lds_b + DecLds<D, NQW>::q_off + (wid * NQ + m) * 1024, qo[m]);
+    for (int m = 0; m < NQ; ++m) dma_piece_at(rq, lds_b + DecLds<D, NQW>::q_off + m * 1024, qo[m]);
   }
-  // This wave's pieces of tile t (absolute index; dead when !live) into slot.
-  __device__ __forceinline__ void issue_tile(const KvSrc& src, uint32_t lds_b, int t, bool live,
-                                             int slot, int wid) const {
+  // Tile t (absolute index) into slot.
+  __device__ __forceinline__ void issue_tile(const KvSrc& src, uint32_t lds_b, int t, int slot) const {
     const bool in_cache = t < src.n_ct;
-    const __amdgpu_buffer_rsrc_t kc = src.kc, kn = src.kn, vc = src.vc, vn = src.vn;
-    const __amdgpu_buffer_rsrc_t rk = in_cache ? kc : kn, rv = in_cache ? vc : vn;
+    const __amdgpu_buffer_rsrc_t rk = in_cache ? src.kc : src.kn, rv = in_cache ? src.vc : src.vn;
     const uint32_t row0 = uint32_t((in_cache ? t : t - src.n_ct) * kBN);
-    const uint32_t bk = live ? row0 * uint32_t(in_cache ? src.c_ss2 : src.k_sl2) : 0x80000000u;
-    const uint32_t bv = live ? row0 * uint32_t(in_cache ? src.c_ss2 : src.v_sl2) : 0x80000000u;
+    const uint32_t bk = row0 * uint32_t(in_cache ? src.c_ss2 : src.k_sl2);
+    const uint32_t bv = row0 * uint32_t(in_cache ? src.c_ss2 : src.v_sl2);
     const uint32_t cmask = in_cache ? ~0u : 0u;
     const uint32_t kt = lds_b + 2 * L::kstage(slot), vt = lds_b + 2 * L::vstage(slot);
 #pragma unroll
-    for (int m = 0; m < NK; ++m) {
-      const uint32_t p = uint32_t(wid + NQW * m) * 1024u;
-      dma_piece_at(rk, kt + p, on[m] + (dc[m] & cmask) + bk);
-    }
+    for (int m = 0; m < PK; ++m) dma_piece_at(rk, kt + m * 1024, on[m] + (dc[m] & cmask) + bk);
 #pragma unroll
-    for (int m = 0; m < NK; ++m) {
-      const uint32_t p = uint32_t(wid + NQW * m) * 1024u;
-      dma_piece_at(rv, vt + p, on[NK + m] + (dc[NK + m] & cmask) + bv);
-    }
+    for (int m = 0; m < PK; ++m)
+      dma_piece_at(rv, vt + m * 1024, on[PK + m] + (dc[PK + m] & cmask) + bv);
   }
 };
 
-// One key tile for one wave from a slot: S^T = K Q^T, softmax, O^T += V^T P^T.
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
+// One half of a key tile for one compute wave: S^T = K Q^T over the tile's
+// keys [32 h, 32 h + 32), softmax, O^T += V^T P^T. Two waves of a query block
+// take the two halves of every tile, each with its own running (max, sum,
+// output), merged after the loop: with seven waves a CU runs two per SIMD,
+// and one wave's exponentials (32 per lane per tile, quarter-rate) overlap
+// the other's MFMAs. (Alone, a wave spent ~2,200 cycles per whole tile,
+// about as long on the exponentials and packing as on its 32 MFMAs.)
 // kb / vb: this lane's operand addresses in the slot (PairAddr plus the
 // slot's offset). The operand reads run ahead of the MFMAs that use them (K
 // fragments four MFMAs ahead, V^T fragments two), and sched_group_barrier
 // keeps that order: left to itself the compiler puts each read right before
 // its MFMA and the wave waits out the LDS latency every time.
 template <int D, typename T>
-__device__ __forceinline__ void dec_tile(const uint32_t (&kb)[D / 16], const uint32_t (&vb)[D / 32],
-                                         const u32x4 (&qr)[D / 16], f32x16 (&acc)[D / 32],
-                                         Softmax& sm, float c, int lim, bool masked) {
+__device__ __forceinline__ void dec_half(int h, const uint32_t (&kb)[D / 16],
+                                         const uint32_t (&vb)[D / 32], const u32x4 (&qr)[D / 16],
+                                         f32x16 (&acc)[D / 32], Softmax& sm, float c, int lim,
+                                         bool masked) {
   constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
-  constexpr int NQ = 2 * KS;  // S MFMAs: half i % 2 (keys 32 (i % 2)..), k-step i / 2
-  constexpr int NP = 4 * DT;  // PV MFMAs: key step i / DT, head_dim tile i % DT
+  constexpr int NQ = KS;      // S MFMAs, one per k-step
+  constexpr int NP = 2 * DT;  // PV MFMAs: key step i / DT (of 16 keys), head_dim tile i % DT
   constexpr int W = 4;        // K fragments in flight
+  const uint32_t hk = uint32_t(h) * 32 * RB;  // the half's first row
   auto kfrag = [&](int i) __attribute__((always_inline)) {
-    return lds_read_b128_at(kb[i / 2] + (i % 2) * 32 * RB);
+    return lds_read_b128_at(kb[i] + hk);
   };
   auto vfrag = [&](int i) __attribute__((always_inline)) {
-    const uint32_t vu = vb[i % DT] + 16 * (i / DT) * RB;
+    const uint32_t vu = vb[i % DT] + hk + 16 * (i / DT) * RB;
     const u32x2 lo = lds_read_tr16_at(vu);
     const u32x2 hi = lds_read_tr16_at(vu + 8 * RB);
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
-  f32x16 s[2] = {f32x16{}, f32x16{}};
+  f32x16 sc = f32x16{};
   u32x4 kf[W];
 #pragma unroll
   for (int i = 0; i < W; ++i) kf[i] = kfrag(i);
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
-    s[i % 2] = Mfma<T>::run(kf[i % W], qr[i / 2], s[i % 2]);
+    sc = Mfma<T>::run(kf[i % W], qr[i], sc);
     if (i + W < NQ) kf[i % W] = kfrag(i + W);
   }
 #pragma unroll
@@ -1803,9 +1810,47 @@ __device__ __forceinline__ void dec_tile(const uint32_t (&kb)[D / 16], const uin
     if (i + W < NQ) __builtin_amdgcn_sched_group_barrier(sg::kDsRead, 1, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  const float mb = softmax_max<D>(s, acc, sm, c, lim, masked);
-  u32x4 pk[4];
-  exp_pack<T>(s, sm, c, mb, pk);
+  // Softmax of the half's 32 keys (lim counts from the half's first key).
+  if (masked) {
+    int lm = lim - 32 * h;
+    asm volatile("" : "+v"(lm));
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (key_hidden(0, r, lm)) sc[r] = -INFINITY;
+  }
+  float tm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+  for (int r = 0; r < 16; ++r) tm[r % 4] = fmaxf(tm[r % 4], sc[r]);
+  const float tmax = xor32_max(fmaxf(fmaxf(tm[0], tm[1]), fmaxf(tm[2], tm[3])));
+  const float m_new = fmaxf(sm.m, tmax);
+  // Lazy rescale (wave-uniform branch): only when some lane's max grew by
+  // more than 2^8. Before anything is accumulated (m = -inf on every lane)
+  // there is nothing to scale: just take the new reference.
+  const bool grow = (m_new - sm.m) * c > 8.0f;
+  if (__any(grow)) {
+    if (!__all(sm.m == -INFINITY)) {
+      const float corr = sm.m == -INFINITY ? 0.f : fast_exp2((sm.m - m_new) * c);
+      sm.l *= corr;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) acc[d] *= corr;
+    }
+    sm.m = m_new;
+  }
+  const float mb = sm.m == -INFINITY ? 0.f : sm.m * c;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sc[r] = fast_exp2(__builtin_fmaf(sc[r], c, -mb));
+  // pk[u][e]: keys 8 u + 2 e, +1 of the half (MFMA B-operand order).
+  u32x4 pk[2];
+  float part[2] = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t pp = Mfma<T>::pack(sc[8 * u + 2 * e], sc[8 * u + 2 * e + 1]);
+      pk[u][e] = pp;
+      part[e & 1] = Mfma<T>::sum2(pp, part[e & 1]);
+    }
+  sm.l += part[0] + part[1];
   __builtin_amdgcn_sched_barrier(0);
   u32x4 vf[2];
   vf[0] = vfrag(0);
@@ -1824,42 +1869,41 @@ __device__ __forceinline__ void dec_tile(const uint32_t (&kb)[D / 16], const uin
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Count this wave in on an LDS counter (once, from lane 0: an add from every
-// lane would be folded into one add of the lane count) after its own LDS
-// reads have completed, and wait until the counter reaches `target`. The other
-// waves of the workgroup count themselves in the same way; they are all
-// resident, so the wait ends.
-__device__ __forceinline__ void lds_rendezvous(int* ctr, int target) {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  if ((threadIdx.x & 63) == 0)
-    __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+// Wait until an LDS word written by another wave of the workgroup reaches
+// `target` (the writer is resident and always gets there).
+__device__ __forceinline__ void lds_wait_at_least(const int* w, int target) {
+  while (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
     __builtin_amdgcn_s_sleep(0);
   asm volatile("" ::: "memory");
 }
 
 template <int D, typename T, int NQW>
-__global__ __launch_bounds__(64 * NQW, 1) void attn_decode_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * (2 * NQW + 1), 1) void attn_decode_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
-  constexpr int NT = 64 * NQW;
+  constexpr int NCW = 2 * NQW;     // compute waves: two per query block (key halves)
+  constexpr int NT = 64 * (NCW + 1);
   constexpr int kRows = 32 * NQW;
   using DL = DecLds<D, NQW>;
-  constexpr int kDecSlots = DL::SL;
   using L = PairLds<D, kDecSlots>;
   using Dma = DecDma<D, NQW>;
+  static_assert(NQW >= 1 && NQW <= 3, "per-wave done counts sync[4, 10)");
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   prefetch_args(a);
 
   const Coord it = locate(a, blockIdx.x, false, 0);  // qtile: the query group
   const int b = it.b, h = it.h;
   const int wid = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const bool producer = wid == NCW;
+  // Compute wave w: query block w % NQW, key half w / NQW of every tile.
+  const int blk = wid % NQW, half = wid / NQW;
   const int lane = int(threadIdx.x) & 63, g = lane >> 5, n = lane & 31;
   const int q0 = it.qtile * a.bm;
   const int q_end = min(q0 + a.bm, a.Lq);
-  const int row = wid * 32 + n;  // row within the query group
+  const int row = blk * 32 + n;  // row within the query group
   const int qi = q0 + row;
-  const bool qvalid = qi < q_end;
-  const bool wave_active = q0 + wid * 32 < q_end;
+  const bool wave_active = !producer && q0 + blk * 32 < q_end;
+  // Rows stored by the half-0 waves, after the halves are merged.
+  const bool qvalid = wave_active && half == 0 && qi < q_end;
   const int cache_len = it.cache_len;
 
   // Tiles over every key any query of the call may see (cache, then all Lk
@@ -1886,73 +1930,149 @@ __global__ __launch_bounds__(64 * NQW, 1) void attn_decode_kernel(AttnArgs a) {
     src.none = make_rsrc(a.q, 0, 0, D);
   }
   const uint32_t smem_b = lds_addr(smem);
+  // sync[0, 3): slot generations; sync[4 + w]: tiles compute wave w is done
+  // with (w < NCW <= 6); sync[10, 13): merge flags.
   int* const sync = reinterpret_cast<int*>(reinterpret_cast<char*>(smem) + DL::sync_off);
-  if (threadIdx.x < 2 * kDecSlots) sync[threadIdx.x] = 0;
-  Dma dma;
-  dma.init(wid, lane, src, int(a.q_sl) * 2);
-  {
-    // This wave's Q rows of [q0, q_end) of head h; rows past them read as zeros.
-    const __amdgpu_buffer_rsrc_t rq =
-        make_rsrc(a.q + b * a.q_sb + int64_t(q0) * a.q_sl + h * a.q_sh, q_end - q0,
-                  int(a.q_sl) * 2, D);
-    dma.issue_q(rq, smem_b, wid);
-  }
-#pragma unroll
-  for (int j = 0; j < kDecSlots; ++j) dma.issue_tile(src, smem_b, t_begin + j, j < nt, j, wid);
-  __syncthreads();  // the counters are zeroed before anyone counts in
-
-  const EndBounds eb = end_bounds(a, q0, q_end - 1);
-  const int kv_min = cache_len + eb.lo, kv_max = cache_len + eb.hi;
-  // Evaluated on every lane (rows past the group clamped): the block-start
-  // reads then stay scalar loads, which the tile waits below do not count.
-  const int my_end = qvalid ? cache_len + visible_end(a, min(qi, a.Lq - 1)) : 0;
-
-  PairAddr<D, kDecSlots> ad;
-  ad.init(smem_b, lane);
+  int* const done = sync + 4;
   f32x16 acc[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
   Softmax sm{-INFINITY, 0.f};
   const float c = a.scale_log2;
-  u32x4 qr[KS];
 
-  // Tile j sits in slot j % kDecSlots. Every wave issues the same number of
-  // pieces per tile, and the refill of tile j + kDecSlots follows tile j, so
-  // when tile j is needed exactly kDecSlots - 1 tiles were issued after it.
-  constexpr int kLead = (kDecSlots - 1) * Dma::per_tile;
-  for (int j = 0; j < nt; ++j) {
-    const int slot = j % kDecSlots, use = j / kDecSlots + 1;
-    __builtin_amdgcn_s_waitcnt((kLead & 15) | ((kLead >> 4) << 14) | (7 << 4));  // vmcnt(kLead)
-    lds_rendezvous(sync + slot, NQW * use);  // every wave's pieces of tile j have landed
-    if (j == 0) {
-      // Q^T operand of this wave's 32 queries (lane: query n, head_dim
-      // [16 s + 8 g, +8) per k-step s), from its K-swizzled Q rows (which
-      // its own vmcnt wait above covers).
-      const uint32_t qb = DL::q_off + wid * 32 * RB - 2 * L::kstage(0);
-      const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
-#pragma unroll
-      for (int s = 0; s < KS; ++s) qr[s] = lds_read_b128_at(ad.k[s] + qb) ^ flip;
-    }
+  // Tiles [0, na) hold keys some row of the group may see: tile starts grow
+  // with j, so they are a prefix. Evaluated by every wave (scalar work; no
+  // memory loads without block starts).
+  const EndBounds eb = end_bounds(a, q0, q_end - 1);
+  const int kv_min = cache_len + eb.lo, kv_max = cache_len + eb.hi;
+  auto tile_start = [&](int j) __attribute__((always_inline)) {
     const int tg = t_begin + j;
-    const bool in_cache = tg < n_ct;
-    const int j0 = in_cache ? tg * kBN : cache_len + (tg - n_ct) * kBN;
-    if (wave_active && j0 < kv_max) {
-      const uint32_t ko = 2 * L::kstage(slot), vo = 2 * (L::vstage(slot) - L::vstage(0));
-      uint32_t kb[KS], vb[DT];
+    return tg < n_ct ? tg * kBN : cache_len + (tg - n_ct) * kBN;
+  };
+
+  if (producer) {
+    // Q rows of [q0, q_end) of head h (rows past them read as zeros), then
+    // the first two tiles; then per tile: wait for its pieces (the next
+    // tile's stay in flight), publish it, refill the slot the previous tile
+    // used once every compute wave is done with it. (The first two tiles go
+    // out before the visible range is known; a tile past it lands unused.)
+    Dma dma;
+    dma.init(lane, src, int(a.q_sl) * 2);
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(a.q + b * a.q_sb + int64_t(q0) * a.q_sl + h * a.q_sh, q_end - q0,
+                  int(a.q_sl) * 2, D);
+    dma.issue_q(rq, smem_b);
+    if (nt > 0) dma.issue_tile(src, smem_b, t_begin, 0);
+    if (nt > 1) dma.issue_tile(src, smem_b, t_begin + 1, 1);
+    int na = 0;
+    while (na < nt && tile_start(na) < kv_max) ++na;
+    __syncthreads();  // the counters are zeroed before anyone uses them
+    for (int j = 0; j < na; ++j) {
+      if (j + 1 < na) wait_vmcnt<Dma::per_tile>();
+      else wait_vmcnt<0>();
+      if (lane == 0)
+        __hip_atomic_store(sync + j % kDecSlots, j / kDecSlots + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (j + 2 < na) {
+        // Tile j - 1 (slot (j + 2) % 3) done by every compute wave: each
+        // wave's own count, since a wave ahead cannot stand in for one behind.
+        if (j >= 1)
+          for (int w = 0; w < NCW; ++w) lds_wait_at_least(done + w, j);
+        dma.issue_tile(src, smem_b, t_begin + j + 2, (j + 2) % kDecSlots);
+      }
+    }
+  } else {
+    if (threadIdx.x < 16) sync[threadIdx.x] = 0;
+    // Visible-key end of this lane's query (both key halves mask with it).
+    const int my_end = wave_active && qi < q_end ? cache_len + visible_end(a, min(qi, a.Lq - 1)) : 0;
+    PairAddr<D, kDecSlots> ad;
+    ad.init(smem_b, lane);
+    int na = 0;
+    while (na < nt && tile_start(na) < kv_max) ++na;
+    const int nw = wave_active ? na : 0;
+    __syncthreads();
+    // Operand addresses and mask of tile j.
+    auto kaddr = [&](int j, uint32_t (&kb)[KS]) __attribute__((always_inline)) {
+      const uint32_t ko = 2 * L::kstage(j % kDecSlots);
 #pragma unroll
       for (int s = 0; s < KS; ++s) kb[s] = ad.k[s] + ko;
+    };
+    auto vaddr = [&](int j, uint32_t (&vb)[DT]) __attribute__((always_inline)) {
+      const uint32_t vo = 2 * (L::vstage(j % kDecSlots) - L::vstage(0));
 #pragma unroll
       for (int d = 0; d < DT; ++d) vb[d] = ad.v[d] + vo;
-      const int lim = (in_cache ? cache_len - j0 : my_end - j0) - 4 * g;
-      const bool masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
-      dec_tile<D, T>(kb, vb, qr, acc, sm, c, lim, masked);
+    };
+    auto limit = [&](int j, int& lim, bool& masked) __attribute__((always_inline)) {
+      const int j0 = tile_start(j);
+      const bool in_cache = t_begin + j < n_ct;
+      lim = (in_cache ? cache_len - j0 : my_end - j0) - 4 * g;
+      masked = in_cache ? j0 + kBN > cache_len : j0 + kBN > kv_min;
+    };
+    if (nw > 0) {
+      u32x4 qr[KS];
+      for (int j = 0; j < nw; ++j) {
+        lds_wait_at_least(sync + j % kDecSlots, j / kDecSlots + 1);  // tile j has landed
+        if (j == 0) {
+          // Q^T operand of the block's 32 queries (lane: query n, head_dim
+          // [16 s + 8 g, +8) per k-step s), from the K-swizzled Q rows.
+          const uint32_t qb = DL::q_off + blk * 32 * RB - 2 * L::kstage(0);
+          const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
+#pragma unroll
+          for (int s = 0; s < KS; ++s) qr[s] = lds_read_b128_at(ad.k[s] + qb) ^ flip;
+        }
+        uint32_t kb[KS], vb[DT];
+        int lim;
+        bool masked;
+        kaddr(j, kb);
+        vaddr(j, vb);
+        limit(j, lim, masked);
+        dec_half<D, T>(half, kb, vb, qr, acc, sm, c, lim, masked);
+        // Done with tile j once this wave's reads of it have returned.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0)
+          __hip_atomic_store(done + wid, j + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
     }
-    // Refill the slot with tile j + kDecSlots once every wave is done with it.
-    lds_rendezvous(sync + kDecSlots + slot, NQW * use);
-    dma.issue_tile(src, smem_b, tg + kDecSlots, j + kDecSlots < nt, slot, wid);
+    if (lane == 0)
+      __hip_atomic_store(done + wid, nt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the last (dead) pieces land before the LDS is reused
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // every tile read before the LDS is reused
+
+  {
+    // Merge the key halves: each half-1 wave hands its (max, sum, output) to
+    // its block's half-0 wave through LDS, in 16-byte vectors laid out
+    // [block][vector][lane] (4 DT vectors of output, then (max, sum)).
+    constexpr int HV = 4 * DT + 1;
+    static_assert(NQW * HV * 64 * 16 <= L::bytes, "the hand-over fits the tile slots");
+    f32x4* const hand = reinterpret_cast<f32x4*>(smem) + blk * HV * 64 + lane;
+    if (wave_active && half == 1) {
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          hand[(4 * d + r4) * 64] = f32x4{acc[d][4 * r4], acc[d][4 * r4 + 1], acc[d][4 * r4 + 2],
+                                          acc[d][4 * r4 + 3]};
+      hand[(HV - 1) * 64] = f32x4{sm.m, sm.l, 0.f, 0.f};
+    }
+    __syncthreads();
+    if (wave_active && half == 0) {
+      f32x4 o1[HV];
+#pragma unroll
+      for (int i = 0; i < HV; ++i) o1[i] = hand[i * 64];
+      const float m1 = o1[HV - 1][0], l1 = o1[HV - 1][1];
+      const float mx = fmaxf(sm.m, m1);
+      const float e0 = sm.m == -INFINITY ? 0.f : fast_exp2((sm.m - mx) * c);
+      const float e1 = m1 == -INFINITY ? 0.f : fast_exp2((m1 - mx) * c);
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[d][r] = acc[d][r] * e0 + o1[4 * d + r / 4][r % 4] * e1;
+      sm.l = sm.l * e0 + l1 * e1;
+      sm.m = mx;
+    }
+    __syncthreads();  // the hand-over area is read before it is reused
+  }
 
   const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
   const float l_tot = xor32_sum(sm.l);
@@ -1961,172 +2081,193 @@ __global__ __launch_bounds__(64 * NQW, 1) void attn_decode_kernel(AttnArgs a) {
     return;
   }
 
-  // Partial of this split: values [split][row][D] and records [split][row]
-  // of the group's workspace area. The lanes hold scattered 8-byte runs of
-  // 32 rows, so the partial is staged in LDS (rows padded by 16 bytes) and
-  // stored as whole rows, 16 bytes per lane: device-scope write-through (sc1)
-  // when the splits merge in this kernel, plain stores for the merge kernel.
+  // Partial of this split, in the group's workspace area: values as the
+  // MFMA registers hold them, one 512-byte piece per (block, d-tile, r4)
+  // with row n's 16 bytes at 16 n (lane n's 4 f16, then lane n + 32's), so
+  // that every store instruction writes 512 contiguous bytes; records
+  // [split][row] (row = 32 block + n) from lanes g == 0. (Row-major values
+  // would take 8-byte pieces of 32 rows per instruction, which the memory
+  // pipeline issues many times slower.)
   const bool in_kernel_merge = a.counters != nullptr;
   const int nrows = q_end - q0;
-  const uint32_t ws_rows = uint32_t(a.bm);
+  const uint32_t ws_rows = uint32_t(kRows);
   const __amdgpu_buffer_rsrc_t rws =
       __builtin_amdgcn_make_buffer_rsrc(a.ws_o + it.pbase * ws_rows * D, (short)0,
                                         int(it.n_splits * ws_rows * D * 2), kBufWord3);
   const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
       a.ws_ml + it.pbase * ws_rows * 4, (short)0, int(it.n_splits * ws_rows * 16), kBufWord3);
-  constexpr int kSc1 = 16;  // cache policy: device scope
+  constexpr int kSc0 = 1, kSc1 = 16;  // cache policy: this XCD's L2, device scope
   constexpr int CR = D / 8;
-  constexpr int SP = 2 * D + 16;  // staging row pitch (bytes)
-  static_assert(kRows * (SP + 16) <= L::bytes, "staging fits the tile slots");
-  char* const stage = reinterpret_cast<char*>(smem);
-  f32x4* const srec = reinterpret_cast<f32x4*>(stage + kRows * SP);
+  u32x2 pw[DT][4];
+  f32x4 prec = f32x4{};
   if (qvalid) {
     const PartialScale ps = partial_scale<D>(acc, l_tot);
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int dim = 32 * d + 8 * r4 + 4 * g;
-        u32x2 w;
-        w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
-        w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
-        *reinterpret_cast<u32x2*>(stage + row * SP + dim * 2) = w;
+        pw[d][r4][0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
+        pw[d][r4][1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
       }
-    if (g == 0) srec[row] = f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
+    prec = f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
   }
-  __syncthreads();
-  for (int u = int(threadIdx.x); u < nrows * CR; u += NT) {
-    const int r = u / CR, ch = u - r * CR;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(stage + r * SP + ch * 16);
-    const uint32_t off = ((uint32_t(it.split) * ws_rows + uint32_t(r)) * D + ch * 8) * 2;
-    if (in_kernel_merge) __builtin_amdgcn_raw_buffer_store_b128(v, rws, off, 0, kSc1);
-    else __builtin_amdgcn_raw_buffer_store_b128(v, rws, off, 0, 0);
-  }
-  for (int r = int(threadIdx.x); r < nrows; r += NT) {
-    const u32x4 v = __builtin_bit_cast(u32x4, srec[r]);
-    const uint32_t off = (uint32_t(it.split) * ws_rows + uint32_t(r)) * 16;
-    if (in_kernel_merge) __builtin_amdgcn_raw_buffer_store_b128(v, rrec, off, 0, kSc1);
-    else __builtin_amdgcn_raw_buffer_store_b128(v, rrec, off, 0, 0);
-  }
+  auto store_partial = [&](auto aux) __attribute__((always_inline)) {
+    if (!qvalid) return;
+    const uint32_t vbase = uint32_t(it.split) * ws_rows * D * 2 + uint32_t(blk) * DT * 2048 +
+                           uint32_t(n) * 16 + uint32_t(g) * 8;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        __builtin_amdgcn_raw_buffer_store_b64(pw[d][r4], rws, vbase + (4 * d + r4) * 512, 0,
+                                              decltype(aux)::value);
+    if (g == 0)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, prec), rrec,
+                                             (uint32_t(it.split) * ws_rows + uint32_t(row)) * 16,
+                                             0, decltype(aux)::value);
+  };
+  store_partial(std::integral_constant<int, 0>{});
   if (!in_kernel_merge) return;
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete at device scope
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have reached this XCD's L2
   __syncthreads();
 
   // Merge, spread over the group: split s merges row chunk s (rows
   // [s nrows / S, (s + 1) nrows / S)) of every split's partial, once all S
-  // partials are stored. Group state, at the group's counter slot:
-  //   gs[0] arrivals, gs[1] workgroups finished with the state, gs[2 + c]
-  //   chunk c claimed.
-  // A workgroup arrives (gs[0] += 1); unless it is the last arrival it polls
-  // gs[0] until all S have arrived, with a time limit, so it never waits
-  // forever on a workgroup that has not been scheduled (one whose CU it
-  // holds). A chunk is merged by whoever claims it first (compare-and-swap):
-  // its owner once all have arrived, or the last arrival, which after its
-  // own chunk claims every chunk still unclaimed -- those of owners that
-  // gave up or have not yet seen the last arrival. Every chunk is therefore
-  // merged exactly once, whatever the schedule. The last workgroup to finish
-  // resets the state to zero for the next call.
+  // partials are stored.
+  //
+  // Arrival. Atomics are coherent across the whole device (measured on
+  // MI355X: adds from workgroups on all eight XCDs to one word all count),
+  // but plain stores reach only the L2 of the XCD that issues them. Group
+  // word w (64-bit, at fs) counts arrivals in bits [0, 16), marks from bit
+  // 16, and the arrivals from XCC x in the nibble at bit 32 + 4 x; fs[2]
+  // counts finished workgroups. A workgroup that sees all S arrivals and no
+  // mark decides from the nibbles: all S on its own XCC means every partial
+  // of the group is in this XCC's L2, and it merges its chunk with loads from
+  // the L2 (sc0, the fast path). Any other outcome takes the slow path. One
+  // that does not see S arrivals within fast_ticks marks the word, by
+  // compare-and-swap and only while arrivals < S, so every workgroup of the
+  // group decides the same way (fast iff the S-th arrival precedes every
+  // mark and the group shares one XCC).
+  //
+  // Slow path, at device scope: every workgroup stores its partial again
+  // with device-scope write-through, then gs[0] counts arrivals, gs[1]
+  // finishes, gs[2 + c] claims chunk c. Unless it is the last arrival, a
+  // workgroup polls gs[0] until all S have arrived, with a time limit, so it
+  // never waits forever on a workgroup that has not been scheduled. A chunk
+  // is merged by whoever claims it first (compare-and-swap): its owner once
+  // all have arrived, or the last arrival, which after its own chunk claims
+  // every chunk still unclaimed. Every chunk is merged exactly once.
+  //
+  // The S-th workgroup to finish with each state resets it to zero.
   const int S = it.n_splits;
-  int32_t* const gs = a.counters + it.pbase * kCounterStride;
-  int* const sh = sync + 2 * kDecSlots;
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(gs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == S - 1;
-    int all = last;
-    if (!last) {
-      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-      for (;;) {
-        if (__hip_atomic_fetch_add(gs, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= S) {
-          all = 1;
-          break;
-        }
-        if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) break;
+  int32_t* const fs = a.counters + it.pbase * kCounterStride;
+  uint64_t* const fw = reinterpret_cast<uint64_t*>(fs);
+  int32_t* const gs = fs + 4;
+  int* const sh = sync + 10;
+  constexpr uint64_t kMark = 1ull << 16;
+  const bool use_fs = a.fast_ticks != 0;
+  if (threadIdx.x == 0 && !use_fs) sh[0] = 0;
+  if (threadIdx.x == 0 && use_fs) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+    const uint64_t mine = 1ull | (1ull << (32 + 4 * xcc));
+    const uint64_t alone = uint64_t(S) << (32 + 4 * xcc);  // all S arrivals from this XCC
+    int fast = -1;
+    uint64_t v = __hip_atomic_fetch_add(fw, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (fast < 0) {
+      const uint64_t arrived = v & (kMark - 1), marks = (v >> 16) & 0xffffull;
+      if (marks != 0) {
+        fast = 0;
+      } else if (arrived == uint64_t(S)) {
+        fast = (v >> 32) == (alone >> 32) ? 1 : 0;
+      } else if (__builtin_amdgcn_s_memrealtime() - t0 > a.fast_ticks) {
+        uint64_t expect = v;
+        if (__hip_atomic_compare_exchange_strong(fw, &expect, v + kMark, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          fast = 0;
+        else
+          v = expect;  // changed meanwhile: decide on the new value
+      } else {
         __builtin_amdgcn_s_sleep(1);
+        v = __hip_atomic_fetch_add(fw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    sh[0] = all;
-    sh[1] = last;
+    sh[0] = fast;
   }
   __syncthreads();
-  const bool all = sh[0] != 0, last = sh[1] != 0;
-  // A chunk has at most kRows / 2 rows (S >= 2). Per chunk: every record and
-  // value load goes out at once; the records go to LDS, where one thread per
-  // row turns them into the row's split weights, and each thread combines its
-  // units (row, 8-dim chunk) from the values it holds.
-  constexpr int UPT = (kRows / 2 * CR + NT - 1) / NT;  // units per thread
-  constexpr int RPT = (kMaxDecSplits * kRows / 2 + NT - 1) / NT;  // records per thread
-  f32x4* const lrec = reinterpret_cast<f32x4*>(smem);                       // [split][row]
-  float* const lcoef = reinterpret_cast<float*>(lrec + kMaxDecSplits * kRows / 2);  // [row][split]
-  int* const lexp = reinterpret_cast<int*>(lcoef + kRows / 2 * kMaxDecSplits);     // [row]
-  static_assert(kMaxDecSplits * kRows / 2 * 20 + kRows / 2 * 4 <= L::bytes, "merge scratch fits");
-  for (int c0 = 0; all && c0 < (last ? S : 1); ++c0) {
-    const int c = it.split + c0 < S ? it.split + c0 : it.split + c0 - S;  // own chunk first
-    __syncthreads();  // the previous chunk's LDS scratch and sh[2] have been read
-    if (threadIdx.x == 0) {
-      int unclaimed = 0;
-      sh[2] = __hip_atomic_compare_exchange_strong(gs + 2 + c, &unclaimed, 1, __ATOMIC_RELAXED,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!sh[2]) continue;
+  const bool fast = sh[0] != 0;
+
+  // A chunk has at most kRows / 2 rows (S >= 2). Per chunk: thread t < rn
+  // loads the records of row t of every split and turns them into the row's
+  // split weights (into LDS); meanwhile thread t loads the values of its units
+  // u = t + NT k < rn CR (row u % rn, 8-dim chunk u / rn: consecutive lanes
+  // take consecutive rows of one chunk, contiguous in the partial) of every
+  // split; after one barrier each thread combines its units. Only threads
+  // with work issue loads, each thread's all at once.
+  constexpr int UPT = (kRows / 2 * CR + NT - 1) / NT;  // units per thread, at most
+  float* const lcoef = reinterpret_cast<float*>(smem);                         // [row][split]
+  int* const lexp = reinterpret_cast<int*>(lcoef + kRows / 2 * kMaxDecSplits);  // [row]
+  static_assert(kRows / 2 * (kMaxDecSplits + 1) * 4 <= L::bytes, "merge scratch fits");
+  auto merge_chunk = [&](int c, auto aux) __attribute__((always_inline)) {
+    constexpr int kAux = decltype(aux)::value;
     const int r_lo = c * nrows / S, rn = (c + 1) * nrows / S - r_lo;
-    // Every load is issued before any is used, with no branch between them
-    // (a guarded load compiles to a wait on every earlier one): splits
-    // sp >= S read past the descriptors' bound and return zeros, and rows
-    // r >= rn re-read the chunk's last row; both go unused.
-    f32x4 rv[RPT];
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int idx = int(threadIdx.x) + NT * i, sp = idx / (kRows / 2);
-      const int r = min(idx % (kRows / 2), rn - 1);
-      rv[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             rrec, (uint32_t(sp) * ws_rows + r_lo + r) * 16, 0, kSc1));
-    }
+    const int nu = rn * CR;
+    const int t = int(threadIdx.x);
+    // Splits sp >= S read past the descriptors' bound and return zeros
+    // (unused), so the loads need no branch between them (a guarded load
+    // compiles to a wait on every earlier one).
     u32x4 val[UPT][kMaxDecSplits];
 #pragma unroll
     for (int k = 0; k < UPT; ++k) {
-      const int u = int(threadIdx.x) + NT * k, r = min(u / CR, rn - 1), ch = u % CR;
+      const int u = t + NT * k;
+      if (u < nu) {
+        const int r = r_lo + u % rn, ch = u / rn;
+        const uint32_t off =
+            uint32_t(r / 32) * DT * 2048 + uint32_t(ch) * 512 + uint32_t(r % 32) * 16;
+#pragma unroll
+        for (int sp = 0; sp < kMaxDecSplits; ++sp)
+          val[k][sp] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         rws, uint32_t(sp) * ws_rows * D * 2 + off, 0, kAux));
+      }
+    }
+    if (t < rn) {
+      f32x4 rec[kMaxDecSplits];
 #pragma unroll
       for (int sp = 0; sp < kMaxDecSplits; ++sp)
-        val[k][sp] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rws, ((uint32_t(sp) * ws_rows + r_lo + r) * D + ch * 8) * 2, 0, kSc1));
-    }
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      const int idx = int(threadIdx.x) + NT * i, sp = idx / (kRows / 2), r = idx % (kRows / 2);
-      if (sp < S && r < rn) lrec[sp * (kRows / 2) + r] = rv[i];
-    }
-    __syncthreads();
-    if (int(threadIdx.x) < rn) {
+        rec[sp] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rrec, (uint32_t(sp) * ws_rows + r_lo + t) * 16, 0, kAux));
       // Row weights: c_s = exp2(m_s - M) l_s / L, taken relative to the largest
       // scale exponent E (applied once at the end).
-      const int r = int(threadIdx.x);
       float mmax = -INFINITY;
       int emax = INT_MIN;
-      for (int sp = 0; sp < S; ++sp) {
-        mmax = fmaxf(mmax, lrec[sp * (kRows / 2) + r][0]);
-        emax = max(emax, int(lrec[sp * (kRows / 2) + r][2]));
+#pragma unroll
+      for (int sp = 0; sp < kMaxDecSplits; ++sp) {
+        mmax = sp < S ? fmaxf(mmax, rec[sp][0]) : mmax;
+        emax = sp < S ? max(emax, int(rec[sp][2])) : emax;
       }
       const float base = mmax == -INFINITY ? 0.f : mmax;
+      float w[kMaxDecSplits];
       float Lsum = 0.f;
-      for (int sp = 0; sp < S; ++sp) {
-        const f32x4 rs = lrec[sp * (kRows / 2) + r];
-        Lsum += fast_exp2(rs[0] - base) * rs[1];
+#pragma unroll
+      for (int sp = 0; sp < kMaxDecSplits; ++sp) {
+        w[sp] = sp < S ? fast_exp2(rec[sp][0] - base) * rec[sp][1] : 0.f;
+        Lsum += w[sp];
       }
       const float invL = 1.0f / Lsum;  // no visible key anywhere: NaN, as the reference
-      for (int sp = 0; sp < S; ++sp) {
-        const f32x4 rs = lrec[sp * (kRows / 2) + r];
-        lcoef[r * kMaxDecSplits + sp] =
-            __builtin_ldexpf(fast_exp2(rs[0] - base) * rs[1] * invL, int(rs[2]) - emax);
-      }
-      lexp[r] = emax;
+#pragma unroll
+      for (int sp = 0; sp < kMaxDecSplits; ++sp)
+        lcoef[t * kMaxDecSplits + sp] =
+            sp < S ? __builtin_ldexpf(w[sp] * invL, int(rec[sp][2]) - emax) : 0.f;
+      lexp[t] = emax;
     }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < UPT; ++k) {
-      const int u = int(threadIdx.x) + NT * k, r = u / CR, ch = u % CR;
-      if (r >= rn) continue;
+      const int u = t + NT * k;
+      if (u >= nu) continue;
+      const int r = u % rn, ch = u / rn;
       float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int sp = 0; sp < kMaxDecSplits; ++sp)
@@ -2147,12 +2288,59 @@ __global__ __launch_bounds__(64 * NQW, 1) void attn_decode_kernel(AttnArgs a) {
       uint16_t* op = a.out + b * a.o_sb + int64_t(q0 + r_lo + r) * a.o_sl + h * a.o_sh + ch * 8;
       __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(op));
     }
+  };
+
+  if (fast) {
+    merge_chunk(it.split, std::integral_constant<int, kSc0>{});
+  } else {
+    store_partial(std::integral_constant<int, kSc1>{});  // again, through to memory
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = __hip_atomic_fetch_add(gs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == S - 1;
+      int all = last;
+      if (!last) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+          if (__hip_atomic_fetch_add(gs, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= S) {
+            all = 1;
+            break;
+          }
+          if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      sh[1] = all;
+      sh[2] = last;
+    }
+    __syncthreads();
+    const bool all = sh[1] != 0, last = sh[2] != 0;
+    for (int c0 = 0; all && c0 < (last ? S : 1); ++c0) {
+      const int c = it.split + c0 < S ? it.split + c0 : it.split + c0 - S;  // own chunk first
+      __syncthreads();  // the previous chunk's LDS scratch and sh[3] have been read
+      if (threadIdx.x == 0) {
+        int unclaimed = 0;
+        sh[3] = __hip_atomic_compare_exchange_strong(gs + 2 + c, &unclaimed, 1, __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!sh[3]) continue;
+      merge_chunk(c, std::integral_constant<int, kSc1>{});
+    }
+    if (threadIdx.x == 0) {
+      // Done with the slow state; the last to get here resets it.
+      if (__hip_atomic_fetch_add(gs + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1) {
+        for (int i = 0; i < 2 + S; ++i)
+          __hip_atomic_store(gs + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
-  if (threadIdx.x == 0) {
-    // Done with the group's state; the last to get here resets it.
-    if (__hip_atomic_fetch_add(gs + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1) {
-      for (int i = 0; i < 2 + S; ++i)
-        __hip_atomic_store(gs + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0 && use_fs) {
+    // Done with the arrival state; the S-th to finish resets it.
+    if (__hip_atomic_fetch_add(fs + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1) {
+      __hip_atomic_store(fw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(fs + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -2270,8 +2458,8 @@ struct Plan {
   int n_qtiles;
   int bm;                    // queries per work item (decode: query-group rows)
   int kernel;                // AttnKernel
-  int nqw;                   // decode: query waves per workgroup (2 or 4)
-  bool merge_kernel;         // decode: splits merged by attn_combine_kernel, not in the kernel
+  int nqw;                   // decode: compute waves per workgroup (2 or 3)
+  int prow;                  // rows per partial in the workspace (decode: 32 per compute block)
   int n_seg;                 // 0 = uniform
   int uniform_splits;
   std::vector<int> seg_b, seg_splits, seg_cache, seg_base, comb_base;
@@ -2316,7 +2504,7 @@ DecodeShape choose_decode(int64_t units, int64_t Lq, const std::vector<int64_t>&
   const double t_chip1 = double(units * all_tiles * tile_bytes) / kChipBytesPerUs;
   DecodeShape best;
   double best_cost = 1e30;
-  for (int64_t nq = cdiv(Lq, 128); nq <= cdiv(Lq, 16); ++nq) {
+  for (int64_t nq = cdiv(Lq, 96); nq <= cdiv(Lq, 16); ++nq) {
     const int64_t rows = cdiv(Lq, nq);
     if (nq > 1 && cdiv(Lq, cdiv(Lq, nq - 1)) == nq) continue;  // same groups as nq - 1
     // Largest split per segment: cap on the tiles one workgroup streams.
@@ -2343,7 +2531,7 @@ DecodeShape choose_decode(int64_t units, int64_t Lq, const std::vector<int64_t>&
       if (cost < best_cost - 1e-9) {
         best_cost = cost;
         best.rows = int(rows);
-        best.nqw = rows <= 64 ? 2 : 4;
+        best.nqw = rows <= 64 ? 2 : 3;
         best.splits = sp;
       }
       if (forced_splits) break;  // one candidate per query grouping
@@ -2404,8 +2592,8 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   if (forced_kernel == kDecode && dec.rows == 0) {
     // Forced onto the decode kernel: the smallest query groups that fit the
     // kernel, splits as forced (or 1), however many workgroups that takes.
-    dec.rows = int(std::min<int64_t>(Lq, 128));
-    dec.nqw = dec.rows <= 64 ? 2 : 4;
+    dec.rows = int(std::min<int64_t>(Lq, 96));
+    dec.nqw = dec.rows <= 64 ? 2 : 3;
     dec.splits.assign(nseg, 1);
     for (int k = 0; k < nseg; ++k)
       dec.splits[k] = int(std::max<int64_t>(1, std::min<int64_t>({forced_splits ? forced_splits : 1,
@@ -2420,7 +2608,6 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     p.kernel = kDecode;
     p.bm = dec.rows;
     p.nqw = dec.nqw;
-    p.merge_kernel = tuning(DX_TUNE_ATTN_MERGE) == 2;
     splits = dec.splits;
   } else {
     int64_t total = 0;
@@ -2471,7 +2658,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     p.uniform_splits = splits[0];
     p.items = B * per_b * p.uniform_splits;
     p.partials = p.uniform_splits > 1 ? p.items : 0;
-    const bool combine = p.kernel != kDecode || p.merge_kernel;
+    const bool combine = p.kernel != kDecode;
     p.comb_blocks = p.uniform_splits > 1 && combine ? B * per_b * combine_bpt(D, p.bm) : 0;
   } else {
     p.n_seg = int(B);
@@ -2484,7 +2671,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
       p.seg_splits.push_back(splits[k]);
       p.seg_cache.push_back(int(cache_lens[b]));
       p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[k]));
-      const bool combine = p.kernel != kDecode || p.merge_kernel;
+      const bool combine = p.kernel != kDecode;
       p.comb_base.push_back(int(p.comb_base.back() + (splits[k] > 1 && combine
                                                           ? per_b * combine_bpt(D, p.bm) : 0)));
       any_split = any_split || splits[k] > 1;
@@ -2499,8 +2686,11 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   const bool has_partials = p.kernel == kDecode ? p.partials > 0 : p.comb_blocks > 0;
   // The counters are the in-kernel merge's; the merge kernel needs none.
   p.counter_bytes = has_partials ? kCounterRegion : 0;
+  // The decode kernel's partial values are laid out as its MFMA registers
+  // hold them (whole 32-row blocks); the others' are row-major, bm rows.
+  p.prow = p.kernel == kDecode ? 32 * p.nqw : p.bm;
   p.ws_bytes = has_partials
-                   ? kCounterRegion + p.partials * p.bm * (D * 2 + 4 * int64_t(sizeof(float)))
+                   ? kCounterRegion + p.partials * p.prow * (D * 2 + 4 * int64_t(sizeof(float)))
                    : 0;
   return p;
 }
@@ -2549,14 +2739,14 @@ hipError_t launch_decode(const AttnArgs& a, int64_t items, hipStream_t st) {
       opt_in_lds(reinterpret_cast<const void*>(&attn_decode_kernel<D, T, NQW>), lds);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL((attn_decode_kernel<D, T, NQW>), dim3(unsigned(items)),
-                     dim3(64 * NQW), lds, st, a);
+                     dim3(64 * (2 * NQW + 1)), lds, st, a);
   return hipGetLastError();
 }
 
 template <int D, typename T>
 hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
   hipError_t e = p.kernel == kDecode
-                     ? (p.nqw == 4 ? launch_decode<D, T, 4>(a, p.items, st)
+                     ? (p.nqw == 3 ? launch_decode<D, T, 3>(a, p.items, st)
                                    : launch_decode<D, T, 2>(a, p.items, st))
                  : p.kernel == kDual   ? launch_main<D, T, 2>(a, p.items, st)
                  : p.kernel == kPaired ? launch_pair<D, T>(a, p.items, st)
@@ -2717,12 +2907,11 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
   // Workspace: [counters (decode)][f16 partial values][fp32 records].
   char* ws = static_cast<char*>(workspace);
-  // Counters only for the in-kernel merge: a null pointer tells the decode
-  // kernel to store plain partials for attn_combine_kernel.
-  a.counters = p.counter_bytes && p.kernel == kDecode && !p.merge_kernel
-                   ? reinterpret_cast<int32_t*>(ws) : nullptr;
+  // The decode kernel's merge state (it always merges its splits itself).
+  a.counters = p.counter_bytes && p.kernel == kDecode ? reinterpret_cast<int32_t*>(ws) : nullptr;
+  a.fast_ticks = tuning(DX_TUNE_ATTN_MERGE) == 2 ? 0u : kFastTicks;
   a.ws_o = p.ws_bytes ? reinterpret_cast<uint16_t*>(ws + p.counter_bytes) : nullptr;
-  a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.bm * D) : nullptr;
+  a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.prow * D) : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
   a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);
   a.kv_group = int(H / Hkv);

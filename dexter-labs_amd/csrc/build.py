@@ -8,7 +8,8 @@ where ``dexter_amd.ops.gfx950._lib`` loads it. Usage::
 
 Flags: ``-O3``; ``-Xclang -target-feature -Xclang -packed-fp32-ops`` keeps the
 compiler from emitting packed fp32 VALU instructions (the host pass warns that
-it does not know the feature; that is harmless).
+it does not know the feature; that is harmless); ``-mllvm
+-amdgpu-mfma-vgpr-form=1`` keeps MFMA accumulators in ordinary VGPRs.
 """
 
 from __future__ import annotations
@@ -35,6 +36,10 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-result",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: kernels with inline assembly
+    # otherwise get them in AGPRs, and every vector op on an accumulator
+    # (the softmax rescale) then costs a copy out and back.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

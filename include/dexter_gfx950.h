@@ -90,8 +90,9 @@ int dx_abi_version(void);
  *   DX_TUNE_NORM_WAVES   waves per row of the adaLN / gated-residual kernels (1..16)
  *   DX_TUNE_QKV_SPLITS   K splits of the fused QKV GEMM (1..16)
  *   DX_TUNE_QKV_WAVES    waves per workgroup of the fused QKV GEMM (2 or 4)
- *   DX_TUNE_ATTN_MERGE   decode split merge: 1 in the kernel, 2 by a separate
- *                        merge kernel
+ *   DX_TUNE_ATTN_MERGE   one-launch decode merge: 1 through the L2 when the
+ *                        splits share an XCD (the default), 2 at device
+ *                        scope only (for tests)
  * Returns DX_EINVAL for an unknown key or an out-of-range value.
  * No reference counterpart (the reference's tuning is Triton's autotuner).
  */

@@ -33,10 +33,10 @@ pytestmark = pytest.mark.gpu
 DT = torch.bfloat16
 
 # (name, TUNE_ATTN_KERNEL, TUNE_ATTN_MERGE): planner default (dual-stream
-# kernel + merge kernel for decode shapes), the one-launch decode kernel with
-# its in-kernel merge, the decode kernel with the merge kernel, and the
-# single-stream and paired-group kernels.
-PATHS = [("default", 0, 0), ("decode", 4, 1), ("decode+merge", 4, 2), ("single", 1, 0),
+# kernel + merge kernel for decode shapes), the one-launch decode kernel
+# (merging through the L2 where its splits share an XCD), the decode kernel
+# merging at device scope only, and the single-stream and paired-group kernels.
+PATHS = [("default", 0, 0), ("decode", 4, 1), ("decode-device", 4, 2), ("single", 1, 0),
          ("paired", 3, 0)]
 
 
