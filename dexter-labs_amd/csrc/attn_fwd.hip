@@ -2071,7 +2071,8 @@ __global__ __launch_bounds__(64 * (2 * NQW + 1), 1) void attn_decode_kernel(Attn
       sm.l = sm.l * e0 + l1 * e1;
       sm.m = mx;
     }
-    __syncthreads();  // the hand-over area is read before it is reused
+    // No barrier needed after the reads: the LDS is next written (merge
+    // scratch) only after the arrival protocol's barriers.
   }
 
   const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
