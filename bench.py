@@ -274,6 +274,26 @@ def run_config(name: str, device, reps: int) -> dict:
     }
 
 
+def run_gemm_ceiling(device, reps: int = 10) -> dict:
+    """The same box's bf16 GEMM rate through torch.matmul (hipBLASLt), 8192^3, timed
+    like the attention configs: the practical MFMA ceiling of this GPU under its power
+    cap, beside which the prefill configs' fraction of nominal peak is read."""
+    import torch
+
+    from dexter_amd.bench import harness
+
+    n = 8192
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(n, n, generator=g).to(torch.bfloat16).to(device)
+    b = torch.randn(n, n, generator=g).to(torch.bfloat16).to(device)
+    for _ in range(3):
+        torch.matmul(a, b)
+    ms = harness.event_time_ms(lambda: torch.matmul(a, b), reps=reps)
+    tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    return {"shape": [n, n, n], "us": ms * 1e3, "tflops": tflops,
+            "pct_mfma_peak": 100 * tflops / PEAK_BF16_TFLOPS, "library": "torch.matmul (hipBLASLt)"}
+
+
 def run_norm(device, layers: int, reps: int) -> dict:
     """adaLN modulation and gated residual (the ops either side of attention in a Wan
     block) at the C1 activation (83 x 3072) and the C2 prefill activation
@@ -471,7 +491,7 @@ def main() -> int:
                     help="seconds of CPU work for the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip C2/C3/C4")
-    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm", "cross", "qkv"],
+    ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm", "cross", "qkv", "gemm"],
                     default=None,
                     help="time one config's attention only (for profiling runs)")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -505,6 +525,10 @@ def main() -> int:
         print(f"copy calibration: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
         del src, dst
 
+    if args.only == "gemm":
+        print(json.dumps({"only": "gemm", **run_gemm_ceiling(device, reps=max(10, args.steps))}),
+              flush=True)
+        return 0
     if args.only in ("norm", "cross", "qkv"):
         run = {"norm": run_norm, "cross": run_cross, "qkv": run_qkv}[args.only]
         res = run(device, args.layers, reps=max(10, args.steps))
@@ -522,8 +546,13 @@ def main() -> int:
              "prologue_C1": head["prologue"],
              "prologue_append_fused_C1": head["prologue_append_fused"]}
     if not args.no_extra:
+        extra["gemm_ceiling"] = run_gemm_ceiling(device)
+        print(f"gemm ceiling: {extra['gemm_ceiling']['tflops']:.0f} TFLOP/s", file=sys.stderr,
+              flush=True)
         for name, reps in (("C2", 20), ("C3", 20), ("C4", 50)):
             extra[name] = run_config(name, device, reps)
+            extra[name]["pct_of_gemm_ceiling"] = (100 * extra[name]["tflops"]
+                                                  / extra["gemm_ceiling"]["tflops"])
             print(f"{name} done: {extra[name]['us']:.1f} us", file=sys.stderr, flush=True)
         extra["norm"] = run_norm(device, args.layers, reps=20)
         print("norm done: " + ", ".join(f"{k} {v['us']:.2f} us" for k, v in extra["norm"].items()
