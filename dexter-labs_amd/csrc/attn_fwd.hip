@@ -609,6 +609,55 @@ __device__ __forceinline__ u32x2 lds_read_tr16_at(uint32_t addr) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// The paired kernel's row area: its BM query rows, K-swizzled (chunk c of
+// row r at c ^ kswz(r)), after the K/V stages. Q arrives there by LDS DMA in
+// whole-row pieces (lane l of piece p: row p RPP + l / CR, physical chunk
+// l % CR), and every wave reads its Q^T operand from it with the K-operand
+// read pattern. After the tile loop, when no DMA targets it any more, each
+// wave stages its 32 result rows there, so that the result leaves as
+// 16-byte row chunks, 64 per instruction, instead of as 8-byte pieces of 32
+// rows each (which the texture path processes one row line at a time).
+template <int D> struct PairRows {
+  using L = PairLds<D>;
+  static constexpr int CR = D / 8, RPP = 64 / CR, RB = 2 * D;
+  static constexpr int off = L::bytes;                          // byte offset in LDS
+  static constexpr int bytes = kBMPair * RB;
+  static constexpr int NPW = kBMPair / RPP / kPairWaves;        // Q pieces per wave
+  static_assert(kBMPair % (RPP * kPairWaves) == 0, "Q pieces deal evenly over the waves");
+  static_assert(off + bytes <= 160 * 1024, "stages and rows fit one workgroup's LDS");
+  // Byte address of logical 16-byte chunk c of row r.
+  __device__ __forceinline__ static uint32_t at(uint32_t lds, int r, int c) {
+    return lds + off + uint32_t(r * RB + 16 * (c ^ L::kswz(r)));
+  }
+  // This wave's Q pieces: rows [0, rows) of the work item; the rest read as
+  // zeros (an offset with bit 31 set is past every descriptor's end; the row
+  // stride alone cannot bound them: a one-row tensor may come with stride 0).
+  __device__ __forceinline__ static void load_q(__amdgpu_buffer_rsrc_t rq, int q_sl2, int rows,
+                                                uint32_t lds, int wid, int lane) {
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
+      const int pc = wid + kPairWaves * i;
+      const int r = pc * RPP + lane / CR, x = lane % CR;
+      const uint32_t o = uint32_t(r) * uint32_t(q_sl2) + uint32_t(16 * (x ^ L::kswz(r)));
+      dma_piece_at(rq, lds + off + pc * 1024, r < rows ? o : 0x80000000u);
+    }
+  }
+  // Rows [r0, r0 + rows) of the area, as staged by one wave (rows <= 32), out
+  // to the rows of a buffer with the given row stride; the wave's other rows
+  // are not written.
+  __device__ __forceinline__ static void store_rows(__amdgpu_buffer_rsrc_t ro, int row_bytes,
+                                                    int rows, uint32_t lds, int r0, int lane) {
+#pragma unroll
+    for (int i = 0; i < 32 / RPP; ++i) {
+      const int r = i * RPP + lane / CR, x = lane % CR;
+      const u32x4 v = lds_read_b128_at(at(lds, r0 + r, x));
+      const uint32_t o = uint32_t(r) * uint32_t(row_bytes) + 16u * x;
+      __builtin_amdgcn_raw_buffer_store_b128(v, ro, int(r < rows ? o : 0x80000000u), 0, 0);
+    }
+  }
+};
+
+
 // Position of a work item (or of a combine block) in the schedule.
 struct Coord {
   int b, h, qtile, split;  // split: key split (work items) or row chunk (combine)
@@ -1482,28 +1531,18 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
     src.none = make_rsrc(a.q, 0, 0, D);
   }
 
-  // Q^T operand (see attn_fwd_kernel): rows past the end load the last row
-  // and are zeroed after the first tile's DMA is out.
-  u32x4 qr[KS];
-  {
-    const uint16_t* qp =
-        a.q + b * a.q_sb + int64_t(min(qi, a.Lq - 1)) * a.q_sl + h * a.q_sh + 8 * g;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + 16 * s);
-  }
+  using Rows = PairRows<D>;
   using Dma = PairDma<D, T>;
   const uint32_t smem_b = lds_addr(smem);
+  // The work item's Q rows into the row area (rows past Lq read as zeros),
+  // then K_0 into stage 0 and V of step -1 (nothing: zeros) into V stage 2.
+  Rows::load_q(make_rsrc(a.q + b * a.q_sb + int64_t(q0) * a.q_sl + h * a.q_sh,
+                         max(a.Lq - q0, 0), int(a.q_sl) * 2, D),
+               int(a.q_sl) * 2, a.Lq - q0, smem_b, wid, lane);
   Dma dma;
   dma.init(wid, lane, src);
-  // K_0 into stage 0; V of step -1 (nothing: zeros) into V stage 2.
 #pragma unroll
   for (int m = 0; m < Dma::NP; ++m) dma.issue(m, src, smem_b, t_begin, nt, 0, -1, 0, 2, wid);
-  {
-    const uint32_t qmask = qvalid ? ~0u : 0u;
-    const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qr[s] = (qr[s] & qmask) ^ flip;
-  }
   const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
   PairAddr<D> ad;
   ad.init(smem_b, lane);
@@ -1519,8 +1558,15 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   // The first MFMA phase runs its PV on V stage 2 (step -1) with P = 0. The
   // V slots above filled that stage with zeros, so whatever an earlier kernel
   // left in LDS (NaN included) contributes exactly 0.
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of K_0 and of V stage 2
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's pieces of Q, K_0 and V stage 2
   __syncthreads();
+  // Q^T operand: row ``row``, k-step s = 16-element chunks 2 s + g.
+  u32x4 qr[KS];
+  {
+    const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = lds_read_b128_at(Rows::at(smem_b, row, 2 * s + g)) ^ flip;
+  }
 
   // The phase program, global phases p = -1 .. 2 nt (2 nt + 2 barriers for
   // every wave). Group 0 runs MFMA phase j (S_j, PV_{j-1}) at p = 2j - 1 and
@@ -1639,8 +1685,54 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 
   const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
   const float l_tot = xor32_sum(sm.l);
-  if (!qvalid) return;
-  store_result<D, T>(a, it, BM, row, qi, g, acc, l_tot, mref);
+  if (!wave_active) return;
+  // Result rows through the row area (every earlier read of it was before
+  // the first phase barrier, and no DMA targets it): each wave packs its 32
+  // rows there, then stores them as whole-row chunks.
+  const int r0 = grp * 128 + wave * 32;
+  const int nrows = min(a.Lq - q0 - r0, 32);  // >= 1: the wave is active
+  uint32_t w[DT][4][2];
+  __amdgpu_buffer_rsrc_t ro;
+  int ro_bytes;
+  if (it.n_splits == 1) {
+    const float inv = 1.0f / l_tot;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        w[d][r4][0] = Mfma<T>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
+        w[d][r4][1] = Mfma<T>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
+      }
+    ro_bytes = int(a.o_sl) * 2;
+    ro = make_rsrc(a.out + it.b * a.o_sb + int64_t(q0 + r0) * a.o_sl + it.h * a.o_sh, nrows,
+                   ro_bytes, D);
+  } else {
+    const int64_t pidx = it.pbase + it.split;
+    const PartialScale ps = partial_scale<D>(acc, l_tot);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        w[d][r4][0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
+        w[d][r4][1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
+      }
+    if (qvalid && g == 0)
+      *reinterpret_cast<f32x4*>(a.ws_ml + (pidx * BM + row) * 4) =
+          f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
+    ro_bytes = D * 2;
+    ro = make_rsrc(a.ws_o + (pidx * BM + r0) * D, nrows, ro_bytes, D);
+  }
+  // Dims 32 d + 8 r4 + 4 g .. + 3 of row ``row``: half g of chunk 4 d + r4.
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+      *reinterpret_cast<lds_u32x2*>(Rows::at(smem_b, row, 4 * d + r4) + 8 * g) =
+          u32x2{w[d][r4][0], w[d][r4][1]};
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
+  Rows::store_rows(ro, ro_bytes, nrows, smem_b, r0, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -2725,7 +2817,7 @@ hipError_t launch_main(const AttnArgs& a, int64_t items, hipStream_t st) {
 
 template <int D, typename T>
 hipError_t launch_pair(const AttnArgs& a, int64_t items, hipStream_t st) {
-  constexpr int lds = PairLds<D>::bytes;
+  constexpr int lds = PairRows<D>::off + PairRows<D>::bytes;
   const hipError_t attr = opt_in_lds(reinterpret_cast<const void*>(&attn_pair_kernel<D, T>), lds);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL((attn_pair_kernel<D, T>), dim3(unsigned(items)), dim3(64 * kPairWaves),

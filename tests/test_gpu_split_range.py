@@ -150,3 +150,22 @@ def test_unordered_block_lists_match_reference(device, built_lib, path, blocks):
         got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c, block_boundaries=bb)
     torch.cuda.synchronize()
     assert_parity(got, _oracle(q, k, v, cache, c, bb), what=f"{name} blocks {blocks}")
+
+
+@pytest.mark.parametrize("path", PATHS, ids=[p[0] for p in PATHS])
+@pytest.mark.parametrize("q_len,k_len,cache_len", [(1, 1, 0), (1, 100, 0), (1, 83, 300),
+                                                   (2, 1, 0), (33, 70, 0)])
+def test_few_query_rows(device, built_lib, path, q_len, k_len, cache_len):
+    """One-row (and few-row) queries on every kernel. The op passes stride 0 for a
+    size-1 dim, so a kernel that moves whole row blocks (Q into LDS, results out of
+    it) must bound them by the row count, not by the stride: with stride 0, every
+    row past the first aliases it (a one-row call once came back NaN)."""
+    _, kern, merge = path
+    q = _rand((2, q_len, 3, 128), device, seed=30)
+    k = _rand((2, k_len, 3, 128), device, seed=31)
+    v = _rand((2, k_len, 3, 128), device, seed=32)
+    cache = _rand((2, 2, cache_len + k_len, 3, 128), device, seed=33) if cache_len else None
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, kern), _lib.tuning(_lib.TUNE_ATTN_MERGE, merge):
+        got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len)
+    ref = _oracle(q, k, v, cache, cache_len)
+    assert_parity(got, ref, what=f"{path[0]} q={q_len} k={k_len} cache={cache_len}")
