@@ -609,50 +609,56 @@ __device__ __forceinline__ u32x2 lds_read_tr16_at(uint32_t addr) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-// The paired kernel's row area: its BM query rows, K-swizzled (chunk c of
-// row r at c ^ kswz(r)), after the K/V stages. Q arrives there by LDS DMA in
-// whole-row pieces (lane l of piece p: row p RPP + l / CR, physical chunk
-// l % CR), and every wave reads its Q^T operand from it with the K-operand
-// read pattern. After the tile loop, when no DMA targets it any more, each
-// wave stages its 32 result rows there, so that the result leaves as
-// 16-byte row chunks, 64 per instruction, instead of as 8-byte pieces of 32
-// rows each (which the texture path processes one row line at a time).
-template <int D> struct PairRows {
+// A row area in LDS: rows of D 16-bit elements, K-swizzled (chunk c of row r
+// at c ^ kswz(r), conflict-free for the K-operand read pattern and for 8-byte
+// writes of 32 rows). The kernels stage their result rows in one after the
+// tile loop, so that the result leaves as 16-byte row chunks, 64 per
+// instruction, instead of as 8-byte pieces of 32 rows each (which the texture
+// path processes one row line at a time); the prefill kernel also receives
+// its Q rows in one, by LDS DMA in whole-row pieces (lane l of piece p: row
+// p RPP + l / CR, physical chunk l % CR).
+template <int D> struct RowArea {
   using L = PairLds<D>;
   static constexpr int CR = D / 8, RPP = 64 / CR, RB = 2 * D;
-  static constexpr int off = L::bytes;                          // byte offset in LDS
-  static constexpr int bytes = kBMPair * RB;
-  static constexpr int NPW = kBMPair / RPP / kPairWaves;        // Q pieces per wave
-  static_assert(kBMPair % (RPP * kPairWaves) == 0, "Q pieces deal evenly over the waves");
-  static_assert(off + bytes <= 160 * 1024, "stages and rows fit one workgroup's LDS");
-  // Byte address of logical 16-byte chunk c of row r.
-  __device__ __forceinline__ static uint32_t at(uint32_t lds, int r, int c) {
-    return lds + off + uint32_t(r * RB + 16 * (c ^ L::kswz(r)));
-  }
-  // This wave's Q pieces: rows [0, rows) of the work item; the rest read as
-  // zeros (an offset with bit 31 set is past every descriptor's end; the row
-  // stride alone cannot bound them: a one-row tensor may come with stride 0).
-  __device__ __forceinline__ static void load_q(__amdgpu_buffer_rsrc_t rq, int q_sl2, int rows,
-                                                uint32_t lds, int wid, int lane) {
-#pragma unroll
-    for (int i = 0; i < NPW; ++i) {
-      const int pc = wid + kPairWaves * i;
-      const int r = pc * RPP + lane / CR, x = lane % CR;
-      const uint32_t o = uint32_t(r) * uint32_t(q_sl2) + uint32_t(16 * (x ^ L::kswz(r)));
-      dma_piece_at(rq, lds + off + pc * 1024, r < rows ? o : 0x80000000u);
-    }
+  // Byte address of logical 16-byte chunk c of row r of the area at ``area``.
+  __device__ __forceinline__ static uint32_t at(uint32_t area, int r, int c) {
+    return area + uint32_t(r * RB + 16 * (c ^ L::kswz(r)));
   }
   // Rows [r0, r0 + rows) of the area, as staged by one wave (rows <= 32), out
   // to the rows of a buffer with the given row stride; the wave's other rows
-  // are not written.
+  // are not written (bounded by the row count, not by the buffer: a one-row
+  // tensor may come with row stride 0).
   __device__ __forceinline__ static void store_rows(__amdgpu_buffer_rsrc_t ro, int row_bytes,
-                                                    int rows, uint32_t lds, int r0, int lane) {
+                                                    int rows, uint32_t area, int r0, int lane) {
 #pragma unroll
     for (int i = 0; i < 32 / RPP; ++i) {
       const int r = i * RPP + lane / CR, x = lane % CR;
-      const u32x4 v = lds_read_b128_at(at(lds, r0 + r, x));
+      const u32x4 v = lds_read_b128_at(at(area, r0 + r, x));
       const uint32_t o = uint32_t(r) * uint32_t(row_bytes) + 16u * x;
       __builtin_amdgcn_raw_buffer_store_b128(v, ro, int(r < rows ? o : 0x80000000u), 0, 0);
+    }
+  }
+};
+
+// The paired kernel's row area: its BM query rows, after the K/V stages.
+template <int D> struct PairRows : RowArea<D> {
+  using A = RowArea<D>;
+  static constexpr int off = PairLds<D>::bytes;                   // byte offset in LDS
+  static constexpr int bytes = kBMPair * A::RB;
+  static constexpr int NPW = kBMPair / A::RPP / kPairWaves;       // Q pieces per wave
+  static_assert(kBMPair % (A::RPP * kPairWaves) == 0, "Q pieces deal evenly over the waves");
+  static_assert(off + bytes <= 160 * 1024, "stages and rows fit one workgroup's LDS");
+  // This wave's Q pieces into the area at ``area``: rows [0, rows) of the
+  // work item; the rest read as zeros (an offset with bit 31 set is past
+  // every descriptor's end).
+  __device__ __forceinline__ static void load_q(__amdgpu_buffer_rsrc_t rq, int q_sl2, int rows,
+                                                uint32_t area, int wid, int lane) {
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
+      const int pc = wid + kPairWaves * i;
+      const int r = pc * A::RPP + lane / A::CR, x = lane % A::CR;
+      const uint32_t o = uint32_t(r) * uint32_t(q_sl2) + uint32_t(16 * (x ^ A::L::kswz(r)));
+      dma_piece_at(rq, area + pc * 1024, r < rows ? o : 0x80000000u);
     }
   }
 };
@@ -1051,6 +1057,63 @@ __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it,
   }
 }
 
+// store_result for a whole wave (32 rows, r0 .. r0 + 31 of the work item's
+// bm), through a row area of the LDS that no other wave is using: each lane
+// packs its row there, then the wave stores whole-row chunks (RowArea).
+// Rows at or past Lq are not written. Every lane of the wave must call it.
+template <int D, typename T>
+__device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coord& it, int bm,
+                                                    int q0, int r0, int g, int lane,
+                                                    const f32x16 (&acc)[D / 32], float l_tot,
+                                                    float mref, uint32_t area) {
+  constexpr int DT = D / 32;
+  using A = RowArea<D>;
+  const int row = r0 + (lane & 31);
+  const int nrows = min(a.Lq - q0 - r0, 32);
+  uint32_t w[DT][4][2];
+  __amdgpu_buffer_rsrc_t ro;
+  int ro_bytes;
+  if (it.n_splits == 1) {
+    const float inv = 1.0f / l_tot;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        w[d][r4][0] = Mfma<T>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
+        w[d][r4][1] = Mfma<T>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
+      }
+    ro_bytes = int(a.o_sl) * 2;
+    ro = make_rsrc(a.out + it.b * a.o_sb + int64_t(q0 + r0) * a.o_sl + it.h * a.o_sh,
+                   max(nrows, 0), ro_bytes, D);
+  } else {
+    const int64_t pidx = it.pbase + it.split;
+    const PartialScale ps = partial_scale<D>(acc, l_tot);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        w[d][r4][0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
+        w[d][r4][1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
+      }
+    if (row - r0 < nrows && g == 0)
+      *reinterpret_cast<f32x4*>(a.ws_ml + (pidx * bm + row) * 4) =
+          f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
+    ro_bytes = D * 2;
+    ro = make_rsrc(a.ws_o + (pidx * bm + r0) * D, max(nrows, 0), ro_bytes, D);
+  }
+  // Dims 32 d + 8 r4 + 4 g .. + 3 of row ``row``: half g of chunk 4 d + r4.
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+      *reinterpret_cast<lds_u32x2*>(A::at(area, row, 4 * d + r4) + 8 * g) =
+          u32x2{w[d][r4][0], w[d][r4][1]};
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
+  A::store_rows(ro, ro_bytes, nrows, area, r0, lane);
+}
+
 template <int D, typename T, int NS>
 __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
@@ -1296,8 +1359,13 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   }
 
   const float l_tot = xor32_sum(sm.l);
-  if (!qvalid) return;
-  store_result<D, T>(a, it, kBM, wave * 32 + n, qi, g, acc, l_tot, mref);
+  if (!wave_active) return;
+  // Result rows through the LDS, now free: the tile buffers of stream 1 (past
+  // the hand-over area) or, with one stream, the tile buffers, whose last
+  // reads and DMA pieces ended at the loop's last barrier.
+  const uint32_t smem_base = lds_addr(smem);
+  store_result_staged<D, T>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref,
+                            smem_base + (NS == 2 ? Lds<D>::bytes : 0));
 }
 
 // ---------------------------------------------------------------------------
@@ -1538,7 +1606,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   // then K_0 into stage 0 and V of step -1 (nothing: zeros) into V stage 2.
   Rows::load_q(make_rsrc(a.q + b * a.q_sb + int64_t(q0) * a.q_sl + h * a.q_sh,
                          max(a.Lq - q0, 0), int(a.q_sl) * 2, D),
-               int(a.q_sl) * 2, a.Lq - q0, smem_b, wid, lane);
+               int(a.q_sl) * 2, a.Lq - q0, smem_b + Rows::off, wid, lane);
   Dma dma;
   dma.init(wid, lane, src);
 #pragma unroll
@@ -1565,7 +1633,8 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   {
     const uint32_t flip = a.negate_q ? 0x80008000u : 0u;  // exact sign flip of both halves
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qr[s] = lds_read_b128_at(Rows::at(smem_b, row, 2 * s + g)) ^ flip;
+    for (int s = 0; s < KS; ++s)
+      qr[s] = lds_read_b128_at(Rows::at(smem_b + Rows::off, row, 2 * s + g)) ^ flip;
   }
 
   // The phase program, global phases p = -1 .. 2 nt (2 nt + 2 barriers for
@@ -1686,53 +1755,10 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
   const float l_tot = xor32_sum(sm.l);
   if (!wave_active) return;
-  // Result rows through the row area (every earlier read of it was before
-  // the first phase barrier, and no DMA targets it): each wave packs its 32
-  // rows there, then stores them as whole-row chunks.
-  const int r0 = grp * 128 + wave * 32;
-  const int nrows = min(a.Lq - q0 - r0, 32);  // >= 1: the wave is active
-  uint32_t w[DT][4][2];
-  __amdgpu_buffer_rsrc_t ro;
-  int ro_bytes;
-  if (it.n_splits == 1) {
-    const float inv = 1.0f / l_tot;
-#pragma unroll
-    for (int d = 0; d < DT; ++d)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        w[d][r4][0] = Mfma<T>::pack(acc[d][4 * r4] * inv, acc[d][4 * r4 + 1] * inv);
-        w[d][r4][1] = Mfma<T>::pack(acc[d][4 * r4 + 2] * inv, acc[d][4 * r4 + 3] * inv);
-      }
-    ro_bytes = int(a.o_sl) * 2;
-    ro = make_rsrc(a.out + it.b * a.o_sb + int64_t(q0 + r0) * a.o_sl + it.h * a.o_sh, nrows,
-                   ro_bytes, D);
-  } else {
-    const int64_t pidx = it.pbase + it.split;
-    const PartialScale ps = partial_scale<D>(acc, l_tot);
-#pragma unroll
-    for (int d = 0; d < DT; ++d)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        w[d][r4][0] = Mfma<f16_t>::pack(acc[d][4 * r4] * ps.k, acc[d][4 * r4 + 1] * ps.k);
-        w[d][r4][1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
-      }
-    if (qvalid && g == 0)
-      *reinterpret_cast<f32x4*>(a.ws_ml + (pidx * BM + row) * 4) =
-          f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
-    ro_bytes = D * 2;
-    ro = make_rsrc(a.ws_o + (pidx * BM + r0) * D, nrows, ro_bytes, D);
-  }
-  // Dims 32 d + 8 r4 + 4 g .. + 3 of row ``row``: half g of chunk 4 d + r4.
-#pragma unroll
-  for (int d = 0; d < DT; ++d)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
-      *reinterpret_cast<lds_u32x2*>(Rows::at(smem_b, row, 4 * d + r4) + 8 * g) =
-          u32x2{w[d][r4][0], w[d][r4][1]};
-    }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
-  Rows::store_rows(ro, ro_bytes, nrows, smem_b, r0, lane);
+  // Result rows through the row area: every earlier read of it was before
+  // the first phase barrier, and no DMA targets it.
+  store_result_staged<D, T>(a, it, BM, q0, grp * 128 + wave * 32, g, lane, acc, l_tot, mref,
+                            smem_b + Rows::off);
 }
 
 // ---------------------------------------------------------------------------
