@@ -90,6 +90,7 @@ struct AttnArgs {
   int causal;
   int n_qtiles;
   int bm;            // queries per work item: 128 (dual-stream decode) or 256 (paired groups)
+  int comb_chunks;   // merge-kernel blocks per work-item group (rows min(bm, Lq) only)
   float scale_log2;  // |softmax scale| * log2(e)
   int negate_q;      // softmax scale < 0: q enters negated (exact), scale as |scale|
   int cache_len;     // uniform mode
@@ -2521,9 +2522,10 @@ template <int D, typename T, int NMAX>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   prefetch_args(a);
   using CS = CombineShape<D>;
-  // Blocks per work-item group: ceil(bm / RPB), as the host sizes the grid
-  // (bm need not be a multiple of RPB: decode query groups).
-  const Coord cd = locate(a, blockIdx.x, true, (a.bm + CS::RPB - 1) / CS::RPB);
+  // Blocks per work-item group: ceil(min(bm, Lq) / RPB), as the host sizes
+  // the grid (no block for rows that no query tile has; bm need not be a
+  // multiple of RPB: decode query groups).
+  const Coord cd = locate(a, blockIdx.x, true, a.comb_chunks);
   const int row = cd.split * CS::RPB + threadIdx.x / CS::TPR;
   const int dim = 4 * (threadIdx.x % CS::TPR);
   const int qi = cd.qtile * a.bm + row;
@@ -2771,6 +2773,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     }
   }
   p.n_qtiles = int(cdiv(Lq, p.bm));
+  const int64_t comb_rows = std::min<int64_t>(p.bm, Lq);  // merge rows per query tile, at most
   const int64_t per_b = H * p.n_qtiles;  // (head, query tile) units per sequence
   if (!cache_lens) {
     p.n_seg = 0;
@@ -2778,7 +2781,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     p.items = B * per_b * p.uniform_splits;
     p.partials = p.uniform_splits > 1 ? p.items : 0;
     const bool combine = p.kernel != kDecode;
-    p.comb_blocks = p.uniform_splits > 1 && combine ? B * per_b * combine_bpt(D, p.bm) : 0;
+    p.comb_blocks = p.uniform_splits > 1 && combine ? B * per_b * combine_bpt(D, comb_rows) : 0;
   } else {
     p.n_seg = int(B);
     p.seg_base.push_back(0);
@@ -2792,7 +2795,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
       p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[k]));
       const bool combine = p.kernel != kDecode;
       p.comb_base.push_back(int(p.comb_base.back() + (splits[k] > 1 && combine
-                                                          ? per_b * combine_bpt(D, p.bm) : 0)));
+                                                          ? per_b * combine_bpt(D, comb_rows) : 0)));
       any_split = any_split || splits[k] > 1;
     }
     p.items = p.seg_base.back();
@@ -3037,6 +3040,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.causal = causal != 0;
   a.n_qtiles = p.n_qtiles;
   a.bm = p.bm;
+  a.comb_chunks = int(combine_bpt(D, std::min<int64_t>(p.bm, Lq)));
   // A negative scale enters as a negated q (exact) and |scale|, so the kernel
   // only ever multiplies scores by a non-negative factor.
   a.negate_q = softmax_scale < 0.f;
