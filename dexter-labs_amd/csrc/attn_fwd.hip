@@ -720,8 +720,18 @@ __device__ __forceinline__ Coord locate(const AttnArgs& a, int idx, bool combine
   const uint32_t per_q = uint32_t(combine ? chunks : c.n_splits);
   int gidx, rank;
   split_index(local, G, a.kv_group > 1, gidx, rank);
-  const uint32_t rq = uint32_t(rank) / per_q;
-  c.split = int(uint32_t(rank) - rq * per_q);
+  uint32_t rq;
+  if (!combine && a.causal == 0 && a.n_blocks == 0 && a.n_qtiles > 1) {
+    // Every query sees every key, so every query tile of a group costs the
+    // same: the tiles of one key split take consecutive ranks and run side by
+    // side on the group's XCD, where they share the split's K/V through the L2.
+    const uint32_t sp = uint32_t(rank) / uint32_t(a.n_qtiles);
+    rq = uint32_t(rank) - sp * uint32_t(a.n_qtiles);
+    c.split = int(sp);
+  } else {
+    rq = uint32_t(rank) / per_q;
+    c.split = int(uint32_t(rank) - rq * per_q);
+  }
   c.qtile = a.n_qtiles - 1 - int(rq);  // heaviest (latest) query tiles first
   if (a.n_seg == 0) {
     const uint32_t bq = uint32_t(gidx) / uint32_t(a.H);
