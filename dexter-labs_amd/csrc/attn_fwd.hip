@@ -618,6 +618,12 @@ __device__ __forceinline__ u32x2 lds_read_tr16_at(uint32_t addr) {
 // path processes one row line at a time); the prefill kernel also receives
 // its Q rows in one, by LDS DMA in whole-row pieces (lane l of piece p: row
 // p RPP + l / CR, physical chunk l % CR).
+// Cache policy of buffer loads and stores (their aux operand) at device
+// scope (sc1): stores go through to memory and loads fetch the device-coherent
+// copy, so workgroups on different XCDs (each with its own L2) see each
+// other's data once the stores have completed.
+constexpr int kScDevice = 16;
+
 template <int D> struct RowArea {
   using L = PairLds<D>;
   static constexpr int CR = D / 8, RPP = 64 / CR, RB = 2 * D;
@@ -629,6 +635,8 @@ template <int D> struct RowArea {
   // to the rows of a buffer with the given row stride; the wave's other rows
   // are not written (bounded by the row count, not by the buffer: a one-row
   // tensor may come with row stride 0).
+  // kAux: the stores' cache policy (0, or kScDevice: through to memory).
+  template <int kAux = 0>
   __device__ __forceinline__ static void store_rows(__amdgpu_buffer_rsrc_t ro, int row_bytes,
                                                     int rows, uint32_t area, int r0, int lane) {
 #pragma unroll
@@ -636,7 +644,7 @@ template <int D> struct RowArea {
       const int r = i * RPP + lane / CR, x = lane % CR;
       const u32x4 v = lds_read_b128_at(at(area, r0 + r, x));
       const uint32_t o = uint32_t(r) * uint32_t(row_bytes) + 16u * x;
-      __builtin_amdgcn_raw_buffer_store_b128(v, ro, int(r < rows ? o : 0x80000000u), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(v, ro, int(r < rows ? o : 0x80000000u), 0, kAux);
     }
   }
 };
@@ -1068,11 +1076,71 @@ __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it,
   }
 }
 
+// Merge of n split-KV partials of one row (records ml, stored values o, one
+// 16-byte record and 4 f16 values per split) into 4 output values:
+//   out = sum_s c_s o_s 2^e_s,  c_s = exp2(m_s - M) l_s / L,  L = sum_s exp2(m_s - M) l_s
+// with M the largest m_s. The sum runs relative to E, the largest e_s, and
+// 2^E is applied once at the end: every coefficient c_s 2^(e_s - E) is <= 1,
+// so no intermediate overflows, and |out| <= max |v| as in the reference. No
+// visible key in any split: L = 0 and the output is NaN, as the reference.
+//
+// The row's split weights c_s 2^(e_s - E) into c (0 for s >= n), returning E.
+// Splits s >= n hold zeros (loads past the buffer bound) and are masked by
+// selects, not branches, so every load is issued before any is used.
+template <int NMAX>
+__device__ __forceinline__ int merge_weights(const f32x4 (&ml)[NMAX], int n, float (&c)[NMAX]) {
+  float mmax = -INFINITY;
+  int emax = INT_MIN;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    mmax = s < n ? fmaxf(mmax, ml[s][0]) : mmax;
+    emax = s < n ? max(emax, int(ml[s][2])) : emax;
+  }
+  const float base = mmax == -INFINITY ? 0.f : mmax;
+  float w[NMAX];
+  float L = 0.f;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    w[s] = s < n ? fast_exp2(ml[s][0] - base) * ml[s][1] : 0.f;
+    L += w[s];
+  }
+  const float invL = 1.0f / L;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s)
+    c[s] = s < n ? __builtin_ldexpf(w[s] * invL, int(ml[s][2]) - emax) : 0.f;
+  return emax;
+}
+
+// One split's term for two values: a += c o (o two packed f16). Every merge
+// adds the splits' terms in split order, so the separate merge kernel and the
+// prefill kernel's own merge round alike.
+__device__ __forceinline__ void merge_add2(float& a0, float& a1, float c, uint32_t o) {
+  a0 += c * to_f32(f16_t{uint16_t(o & 0xffffu)});
+  a1 += c * to_f32(f16_t{uint16_t(o >> 16)});
+}
+
+template <int NMAX>
+__device__ __forceinline__ f32x4 merge_partials(const f32x4 (&ml)[NMAX], const u32x2 (&o)[NMAX],
+                                                int n) {
+  float c[NMAX];
+  const int emax = merge_weights(ml, n, c);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    merge_add2(acc[0], acc[1], c[s], o[s][0]);
+    merge_add2(acc[2], acc[3], c[s], o[s][1]);
+  }
+  return f32x4{__builtin_ldexpf(acc[0], emax), __builtin_ldexpf(acc[1], emax),
+               __builtin_ldexpf(acc[2], emax), __builtin_ldexpf(acc[3], emax)};
+}
+
 // store_result for a whole wave (32 rows, r0 .. r0 + 31 of the work item's
 // bm), through a row area of the LDS that no other wave is using: each lane
 // packs its row there, then the wave stores whole-row chunks (RowArea).
 // Rows at or past Lq are not written. Every lane of the wave must call it.
-template <int D, typename T>
+// kAux: cache policy of the partial stores of a split work item (0, or
+// kScDevice for a merge by another workgroup of the group in the same launch).
+template <int D, typename T, int kAux = 0>
 __device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coord& it, int bm,
                                                     int q0, int r0, int g, int lane,
                                                     const f32x16 (&acc)[D / 32], float l_tot,
@@ -1107,8 +1175,10 @@ __device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coo
         w[d][r4][1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * ps.k, acc[d][4 * r4 + 3] * ps.k);
       }
     if (row - r0 < nrows && g == 0)
-      *reinterpret_cast<f32x4*>(a.ws_ml + (pidx * bm + row) * 4) =
-          f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f};
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(u32x4, f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(ps.e), 0.f}),
+          __builtin_amdgcn_make_buffer_rsrc(a.ws_ml + pidx * bm * 4, (short)0, bm * 16, kBufWord3),
+          row * 16, 0, kAux);
     ro_bytes = D * 2;
     ro = make_rsrc(a.ws_o + (pidx * bm + r0) * D, max(nrows, 0), ro_bytes, D);
   }
@@ -1122,7 +1192,7 @@ __device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coo
           u32x2{w[d][r4][0], w[d][r4][1]};
     }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's rows are in LDS
-  A::store_rows(ro, ro_bytes, nrows, area, r0, lane);
+  A::template store_rows<kAux>(ro, ro_bytes, nrows, area, r0, lane);
 }
 
 template <int D, typename T, int NS>
@@ -1563,6 +1633,123 @@ __device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32
   }
 }
 
+// Merge state of each work-item group (arrival and finish counters, chunk
+// claims), indexed by the group's first partial, in a region of fixed size at
+// the start of every attention workspace, so that no plan's partials ever
+// overlap another plan's state. Zero before a launch, zero after it.
+constexpr int kCounterStride = 16;           // ints per group state (arrivals, finished, claims)
+constexpr int kCounterSlots = 4096;          // partials a launch that merges in-kernel may have
+constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
+// Key splits of a paired-kernel work-item group merged in the kernel itself,
+// with no merge launch: every split stores its partial at device scope
+// (kScDevice), waits until the stores have completed and arrives on the
+// group's 64-bit counter (the arrival count in the low word, the arrivals from
+// XCD x in the nibble at bit 32 + 4 x); the split that brings the count to
+// n_splits resets the counter and merges all the group's partials into the
+// output, and the others are done. No workgroup ever waits for another, so
+// the order and placement in which the splits run do not matter. When every
+// split ran on the merging workgroup's XCD, the partials are read from that
+// XCD's L2 (kScXcd), else from memory (kScDevice). Groups of more than
+// kPMergeSplits splits take the separate merge kernel instead.
+constexpr int kPMergeSplits = 8;
+// Cache policy of loads of data that workgroups of this XCD stored (sc0):
+// past this CU's L1 to the XCD's L2, which holds every such store.
+constexpr int kScXcd = 1;
+
+// The merge, by the last split: thread t < nrows turns row t's records into
+// the split weights (into LDS) while every thread's loads of its units (row,
+// 8 dims: 16 bytes) of the first splits are in flight; then each thread adds
+// the splits' terms in split order, two splits per batch of loads, with the
+// merge kernel's arithmetic (merge_weights, merge_add2). kAux: cache policy
+// of the loads.
+template <int D, typename T, int kAux>
+__device__ __forceinline__ void pair_merge_group(const AttnArgs& a, const Coord& it, int q0,
+                                                 int nrows, uint16_t* smem) {
+  constexpr int CR = D / 8;               // 16-byte units per row
+  constexpr int NT = 64 * kPairWaves;
+  constexpr int UPT = kBMPair * CR / NT;  // units per thread
+  constexpr int SB = 2;                   // splits per batch of loads
+  static_assert(kBMPair * CR % NT == 0 && kBMPair <= NT, "units deal evenly; a thread per row");
+  static_assert(kPMergeSplits % SB == 0, "whole batches");
+  const int t = int(threadIdx.x);
+  const int S = it.n_splits;
+  const uint32_t rows = uint32_t(a.bm);
+  // Bounded by the group's S partials: loads of splits s >= S return zeros.
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + it.pbase * a.bm * 4, (short)0, int(uint32_t(S) * rows * 16), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rval = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o + it.pbase * a.bm * D, (short)0, int(uint32_t(S) * rows * D * 2), kBufWord3);
+  float* const lc = reinterpret_cast<float*>(smem);                   // [row][kPMergeSplits]
+  int* const le = reinterpret_cast<int*>(lc + kBMPair * kPMergeSplits);  // [row] exponent E
+
+  f32x4 ml[kPMergeSplits];
+  {
+    const uint32_t base = t < nrows ? uint32_t(t) * 16 : 0x80000000u;  // past every bound
+#pragma unroll
+    for (int s = 0; s < kPMergeSplits; ++s)
+      ml[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rrec, base + uint32_t(s) * rows * 16, 0, kAux));
+  }
+  u32x4 v[UPT][SB];
+  auto load_batch = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      const int u = t + NT * k, r = u / CR, ch = u % CR;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const uint32_t off = r < nrows ? (uint32_t(s0 + j) * rows + uint32_t(r)) * (D * 2) +
+                                             uint32_t(ch) * 16
+                                       : 0x80000000u;  // past every bound: zeros
+        v[k][j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rval, off, 0, kAux));
+      }
+    }
+  };
+  load_batch(0);
+  {
+    float c[kPMergeSplits];
+    const int emax = merge_weights(ml, S, c);
+    if (t < nrows) {
+#pragma unroll
+      for (int s = 0; s < kPMergeSplits; ++s) lc[t * kPMergeSplits + s] = c[s];
+      le[t] = emax;
+    }
+  }
+  __syncthreads();
+  float acc[UPT][8];
+#pragma unroll
+  for (int k = 0; k < UPT; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
+  for (int s0 = 0; s0 < S; s0 += SB) {
+    if (s0 > 0) load_batch(s0);
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      const int r = (t + NT * k) / CR;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const float cs = lc[r * kPMergeSplits + s0 + j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) merge_add2(acc[k][2 * e], acc[k][2 * e + 1], cs, v[k][j][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < UPT; ++k) {
+    const int u = t + NT * k, r = u / CR, ch = u % CR;
+    if (r < nrows) {
+      const int emax = le[r];
+      u32x4 packed;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        packed[e] = Mfma<T>::pack(__builtin_ldexpf(acc[k][2 * e], emax),
+                                  __builtin_ldexpf(acc[k][2 * e + 1], emax));
+      uint16_t* op = a.out + it.b * a.o_sb + int64_t(q0 + r) * a.o_sl + it.h * a.o_sh + ch * 8;
+      *reinterpret_cast<u32x4*>(op) = packed;
+    }
+  }
+}
+
 template <int D, typename T>
 __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs a) {
   constexpr int KS = D / 16, DT = D / 32;
@@ -1765,11 +1952,47 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 
   const float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
   const float l_tot = xor32_sum(sm.l);
-  if (!wave_active) return;
   // Result rows through the row area: every earlier read of it was before
   // the first phase barrier, and no DMA targets it.
-  store_result_staged<D, T>(a, it, BM, q0, grp * 128 + wave * 32, g, lane, acc, l_tot, mref,
-                            smem_b + Rows::off);
+  const uint32_t area = smem_b + Rows::off;
+  const int r0 = grp * 128 + wave * 32;
+  if (a.counters == nullptr || it.n_splits == 1) {
+    if (!wave_active) return;
+    store_result_staged<D, T>(a, it, BM, q0, r0, g, lane, acc, l_tot, mref, area);
+    return;
+  }
+  // Split, merged in this launch (pair_merge_group): arrive once this
+  // workgroup's partial is stored; the last of the group merges.
+  if (wave_active)
+    store_result_staged<D, T, kScDevice>(a, it, BM, q0, r0, g, lane, acc, l_tot, mref, area);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed at device scope
+  __syncthreads();
+  // The flag sits in the last word of the K/V stages (idle after the loop),
+  // clear of the merge's weights at the start of the LDS.
+  int* const last = reinterpret_cast<int*>(smem) + PairLds<D>::bytes / 4 - 1;
+  static_assert(kBMPair * (kPMergeSplits + 1) * 4 < PairLds<D>::bytes, "merge scratch fits");
+  static_assert(kPMergeSplits < 16, "an XCD's arrivals fit its nibble");
+  if (threadIdx.x == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+    uint64_t* const cnt = reinterpret_cast<uint64_t*>(a.counters + it.pbase * kCounterStride);
+    const uint64_t mine = 1ull | (1ull << (32 + 4 * xcc));
+    const uint64_t v =
+        __hip_atomic_fetch_add(cnt, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    const uint64_t n = uint64_t(it.n_splits);
+    int state = 0;  // 0: not the last; 1: the last, every split on this XCD; 2: the last
+    if ((v & 0xffffffffull) == n) {
+      state = (v >> 32) == (n << (4 * xcc)) ? 1 : 2;
+      __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *last = state;
+  }
+  __syncthreads();
+  const int state = *last;
+  if (state == 0) return;
+  const int nrows = min(BM, a.Lq - q0);
+  if (state == 1) pair_merge_group<D, T, kScXcd>(a, it, q0, nrows, smem);
+  else pair_merge_group<D, T, kScDevice>(a, it, q0, nrows, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1802,13 +2025,6 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 // merges one row chunk of all the group's partials once all have arrived.
 // ---------------------------------------------------------------------------
 constexpr int kMaxDecSplits = 8;
-// Merge state of each work-item group (arrival and finish counters, chunk
-// claims), indexed by the group's first partial, in a region of fixed size at
-// the start of every attention workspace, so that no plan's partials ever
-// overlap another plan's state. Zero before a launch, zero after it.
-constexpr int kCounterStride = 16;           // ints per group state (arrivals, finished, claims)
-constexpr int kCounterSlots = 4096;          // partials a decode launch may have
-constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
 // Poll limit of a workgroup waiting for its group's other splits:
 // s_memrealtime ticks (100 MHz), 50 us. Reached only when a split cannot be
 // scheduled; the last arrival then merges the waiting workgroup's rows.
@@ -2480,48 +2696,6 @@ template <int D> struct CombineShape {
   static constexpr int RPB = 256 / TPR;  // rows per block
 };
 
-// Merge of n split-KV partials of one row (records ml, stored values o, one
-// 16-byte record and 4 f16 values per split) into 4 output values:
-//   out = sum_s c_s o_s 2^e_s,  c_s = exp2(m_s - M) l_s / L,  L = sum_s exp2(m_s - M) l_s
-// with M the largest m_s. The sum runs relative to E, the largest e_s, and
-// 2^E is applied once at the end: every coefficient c_s 2^(e_s - E) is <= 1,
-// so no intermediate overflows, and |out| <= max |v| as in the reference. No
-// visible key in any split: L = 0 and the output is NaN, as the reference.
-template <int NMAX>
-__device__ __forceinline__ f32x4 merge_partials(const f32x4 (&ml)[NMAX], const u32x2 (&o)[NMAX],
-                                                int n) {
-  // Splits s >= n hold zeros (loads past the buffer bound) and are masked
-  // by selects, not branches, so every load is issued before any is used.
-  float mmax = -INFINITY;
-  int emax = INT_MIN;
-#pragma unroll
-  for (int s = 0; s < NMAX; ++s) {
-    mmax = s < n ? fmaxf(mmax, ml[s][0]) : mmax;
-    emax = s < n ? max(emax, int(ml[s][2])) : emax;
-  }
-  const float base = mmax == -INFINITY ? 0.f : mmax;
-  float w[NMAX];
-  float L = 0.f;
-#pragma unroll
-  for (int s = 0; s < NMAX; ++s) {
-    w[s] = s < n ? fast_exp2(ml[s][0] - base) * ml[s][1] : 0.f;
-    L += w[s];
-  }
-  const float invL = 1.0f / L;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < NMAX; ++s) {
-    const float c = s < n ? __builtin_ldexpf(w[s] * invL, int(ml[s][2]) - emax) : 0.f;
-    acc[0] += c * to_f32(f16_t{uint16_t(o[s][0] & 0xffffu)});
-    acc[1] += c * to_f32(f16_t{uint16_t(o[s][0] >> 16)});
-    acc[2] += c * to_f32(f16_t{uint16_t(o[s][1] & 0xffffu)});
-    acc[3] += c * to_f32(f16_t{uint16_t(o[s][1] >> 16)});
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) acc[e] = __builtin_ldexpf(acc[e], emax);
-  return acc;
-}
-
 // Merge split-KV partials (merge_partials). Each thread owns 4 consecutive
 // dims of a row and issues all NMAX (>= the group's split count) record and
 // value loads before combining: buffer descriptors bounded by the group's
@@ -2595,7 +2769,8 @@ struct Plan {
   int uniform_splits;
   std::vector<int> seg_b, seg_splits, seg_cache, seg_base, comb_base;
   int64_t items, comb_blocks, partials;
-  int64_t counter_bytes;     // decode: arrival counters at the start of the workspace
+  int64_t counter_bytes;     // arrival counters at the start of the workspace
+  bool pmerge;               // paired kernel: splits merged in the kernel (no merge launch)
   int64_t ws_bytes;
 };
 
@@ -2813,8 +2988,8 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     p.partials = any_split ? p.items : 0;
   }
   // Workspace of any plan with partials: the counter region (kCounterRegion
-  // bytes, used by the decode kernel only), the f16 partial values, then the
-  // fp32 records {m, l, e, 0}.
+  // bytes, used by the kernels that merge in-kernel), the f16 partial values,
+  // then the fp32 records {m, l, e, 0}.
   const bool has_partials = p.kernel == kDecode ? p.partials > 0 : p.comb_blocks > 0;
   // The counters are the in-kernel merge's; the merge kernel needs none.
   p.counter_bytes = has_partials ? kCounterRegion : 0;
@@ -2824,6 +2999,13 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   p.ws_bytes = has_partials
                    ? kCounterRegion + p.partials * p.prow * (D * 2 + 4 * int64_t(sizeof(float)))
                    : 0;
+  // The paired kernel merges its splits itself (pair_merge_group) when no
+  // group has more than kPMergeSplits and the counters cover every group.
+  int most = p.uniform_splits;
+  for (int sk : p.seg_splits) most = std::max(most, sk);
+  p.pmerge = p.kernel == kPaired && has_partials && most <= kPMergeSplits &&
+             p.partials <= kCounterSlots && tuning(DX_TUNE_ATTN_PMERGE) != 1;
+  if (p.pmerge) p.comb_blocks = 0;
   return p;
 }
 
@@ -3037,10 +3219,13 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.cv = cache ? static_cast<const uint16_t*>(cache) + c_plane : nullptr;
   a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh;
   a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
-  // Workspace: [counters (decode)][f16 partial values][fp32 records].
+  // Workspace: [counters][f16 partial values][fp32 records].
   char* ws = static_cast<char*>(workspace);
-  // The decode kernel's merge state (it always merges its splits itself).
-  a.counters = p.counter_bytes && p.kernel == kDecode ? reinterpret_cast<int32_t*>(ws) : nullptr;
+  // The merge state of kernels that merge their splits themselves: the
+  // decode kernel always, the paired kernel when planned so.
+  a.counters = p.counter_bytes && (p.kernel == kDecode || p.pmerge)
+                   ? reinterpret_cast<int32_t*>(ws)
+                   : nullptr;
   a.fast_ticks = tuning(DX_TUNE_ATTN_MERGE) == 2 ? 0u : kFastTicks;
   a.ws_o = p.ws_bytes ? reinterpret_cast<uint16_t*>(ws + p.counter_bytes) : nullptr;
   a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.prow * D) : nullptr;

@@ -16,13 +16,13 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
 # dx_set_tuning keys (launch-schedule overrides for measurement and tests).
 (TUNE_ATTN_SPLITS, TUNE_ATTN_KERNEL, TUNE_NORM_WAVES, TUNE_QKV_SPLITS, TUNE_QKV_WAVES,
- TUNE_ATTN_MERGE) = range(6)
+ TUNE_ATTN_MERGE, TUNE_ATTN_PMERGE) = range(7)
 
 _DTYPE_CODE = {torch.bfloat16: DX_BF16, torch.float16: DX_F16, torch.float32: DX_F32,
                torch.int32: DX_I32, torch.int64: DX_I64}

@@ -76,7 +76,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 8
+#define DX_ABI_VERSION 9
 
 /*
  * Launch-schedule overrides, for measurement and tests only: process-wide,
@@ -93,6 +93,10 @@ int dx_abi_version(void);
  *   DX_TUNE_ATTN_MERGE   one-launch decode merge: 1 through the L2 when the
  *                        splits share an XCD (the default), 2 at device
  *                        scope only (for tests)
+ *   DX_TUNE_ATTN_PMERGE  paired prefill with key splits: 1 merges them in a
+ *                        separate merge kernel, 2 in the prefill kernel (the
+ *                        last split of each query tile to finish merges all
+ *                        of its partials; the default)
  * Returns DX_EINVAL for an unknown key or an out-of-range value.
  * No reference counterpart (the reference's tuning is Triton's autotuner).
  */
@@ -102,7 +106,8 @@ int dx_abi_version(void);
 #define DX_TUNE_QKV_SPLITS 3
 #define DX_TUNE_QKV_WAVES 4
 #define DX_TUNE_ATTN_MERGE 5
-#define DX_TUNE_KEYS 6
+#define DX_TUNE_ATTN_PMERGE 6
+#define DX_TUNE_KEYS 7
 int dx_set_tuning(int key, int value);
 
 /*
@@ -184,8 +189,9 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  * out may be strided like q. cache may be NULL when cache_len == 0.
  * workspace must hold dx_attention_workspace_bytes(...) bytes for the same
  * shape (it may be NULL when that is 0). Its first 256 KiB hold the
- * one-launch decode kernel's arrival counters (DX_TUNE_ATTN_KERNEL 4 with
- * the in-kernel merge): they must be zero before a workspace is first used,
+ * arrival counters of the kernels that merge key splits in the same launch
+ * (the prefill kernel by default, the one-launch decode kernel under
+ * DX_TUNE_ATTN_KERNEL 4): they must be zero before a workspace is first used,
  * and every completed call leaves them zero. The rest needs no
  * initialisation. Calls that share a workspace must not overlap.
  * Replaces: ops/gfx1151/attention/blockwise_causal.py:146-173.

@@ -1,0 +1,157 @@
+"""Key splits of the paired prefill kernel merged inside the kernel (MI355X).
+
+With key splits, each split of a (batch, head, query tile) group leaves a
+partial output; by default the split of the group that finishes last merges
+them all in the same launch (``DX_TUNE_ATTN_PMERGE`` 2), and the separate merge
+kernel (``DX_TUNE_ATTN_PMERGE`` 1) remains for groups of more than eight
+splits. Both merges add the splits' terms in the same order with the same
+arithmetic, so their outputs must agree bit for bit; the merged result is also
+held to the north-star bar against the oracle
+(``python/dexter/ops/reference/attention.py:71-77``). The arrival counters
+must come back to zero after every call, which repeated calls and graph
+replays on the same workspace check.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import dexter_amd.ops as ops
+from dexter_amd.bench import harness
+from dexter_amd.ops.gfx950 import _lib
+from oracle import attention as oatt
+
+from _util import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+IN_KERNEL, MERGE_KERNEL = 2, 1
+
+
+def _rand(shape, device, dtype=torch.bfloat16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dtype).to(device)
+
+
+def _oracle(q, k, v, cache, cache_len, bb=None):
+    return oatt.blockwise_causal_attention(
+        q.cpu(), k.cpu(), v.cpu(), None if cache is None else cache.cpu(), cache_len,
+        None if bb is None else bb.cpu(), None, False, keep_fp32=True)
+
+
+def _paired(fn, merge, splits=0):
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, 3), _lib.tuning(_lib.TUNE_ATTN_PMERGE, merge), \
+            _lib.tuning(_lib.TUNE_ATTN_SPLITS, splits):
+        out = fn()
+    torch.cuda.synchronize()
+    return out
+
+
+# (q_len, new keys, cache_len, heads, head_dim, dtype): two query tiles with a
+# partial second one, a single partial tile, one query row, head_dim 64, f16.
+# Head counts that are not multiples of 8 spread a group's splits over several
+# XCDs (merged from memory); 8 keeps them on one (merged through its L2).
+SHAPES = [(300, 300, 700, 8, 128, torch.bfloat16), (145, 145, 900, 5, 128, torch.bfloat16),
+          (1, 1, 400, 4, 128, torch.bfloat16), (300, 300, 500, 8, 64, torch.bfloat16),
+          (257, 257, 600, 3, 128, torch.float16)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"q{s[0]}-c{s[2]}-h{s[3]}-d{s[4]}-{str(s[5])[6:]}"
+                                               for s in SHAPES])
+@pytest.mark.parametrize("splits", [2, 3, 5, 8])
+def test_in_kernel_merge_matches_merge_kernel(device, built_lib, shape, splits):
+    lq, lk, c, h, d, dt = shape
+    q = _rand((1, lq, h, d), device, dt, seed=400)
+    k = _rand((1, lk, h, d), device, dt, seed=401)
+    v = _rand((1, lk, h, d), device, dt, seed=402)
+    cache = _rand((2, 1, c + lk, h, d), device, dt, seed=403)
+
+    def call():
+        return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+
+    got = _paired(call, IN_KERNEL, splits)
+    ref = _paired(call, MERGE_KERNEL, splits)
+    assert torch.equal(got, ref), f"splits={splits}: in-kernel merge differs from the merge kernel"
+    if dt == torch.bfloat16:
+        assert_parity(got, _oracle(q, k, v, cache, c), what=f"{shape} splits={splits}")
+
+
+def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib):
+    """No cache and no mask (cross-attention), then a block list over a cache."""
+    q = _rand((2, 300, 4, 128), device, seed=410)
+    k, v = _rand((2, 700, 4, 128), device, seed=411), _rand((2, 700, 4, 128), device, seed=412)
+    for splits in (2, 4, 7):
+        got = _paired(lambda: ops.blockwise_causal_attention(q, k, v), IN_KERNEL, splits)
+        ref = _paired(lambda: ops.blockwise_causal_attention(q, k, v), MERGE_KERNEL, splits)
+        assert torch.equal(got, ref), f"cross splits={splits}"
+        assert_parity(got, _oracle(q, k, v, None, 0), what=f"cross splits={splits}")
+    cache = _rand((2, 2, 1000, 4, 128), device, seed=413)
+    kn, vn = k[:, :300].contiguous(), v[:, :300].contiguous()
+    bb = torch.tensor([0, 100, 200], dtype=torch.int32, device=device)
+
+    def blocks():
+        return ops.blockwise_causal_attention(q, kn, vn, kv_cache=cache, cache_len=700,
+                                              block_boundaries=bb)
+
+    got = _paired(blocks, IN_KERNEL, 3)
+    assert torch.equal(got, _paired(blocks, MERGE_KERNEL, 3)), "block list splits=3"
+    assert_parity(got, _oracle(q, kn, vn, cache, 700, bb), what="block list splits=3")
+
+
+def test_in_kernel_merge_ragged_batch(device, built_lib):
+    """The C4 ragged lengths on the paired kernel with the planner's splits
+    (several per long sequence, one for the short ones)."""
+    lens = [0, 332, 1245, 3237]
+    h, d = 8, 128
+    q, k, v = (_rand((4, 99, h, d), device, seed=420 + i) for i in range(3))
+    cache = _rand((2, 4, max(lens), h, d), device, seed=423)
+    bb = torch.tensor([0, 83], dtype=torch.int32, device=device)
+
+    def call():
+        return ops.blockwise_causal_attention_varlen(q, k, v, kv_cache=cache, cache_lens=lens,
+                                                     block_boundaries=bb)
+
+    got = _paired(call, IN_KERNEL)
+    assert torch.equal(got, _paired(call, MERGE_KERNEL)), "ragged batch"
+    for i, c in enumerate(lens):
+        assert_parity(got[i:i + 1], _oracle(q[i:i + 1], k[i:i + 1], v[i:i + 1],
+                                            cache[:, i:i + 1], c, bb), what=f"seq {i}")
+
+
+@pytest.mark.parametrize("h", [8, 5])
+def test_in_kernel_merge_repeats_and_graph_replays(device, built_lib, h):
+    """Calls of different split counts one after another on the same workspace,
+    then a captured call replayed with eager calls in between: every result
+    equals the merge kernel's (a counter left nonzero would skip or repeat a
+    group's merge). With 8 heads every group's splits share an XCD (merged
+    through its L2); with 5 they are spread over several (merged from memory)."""
+    lq, c, d = 300, 600, 128
+    ins = [(_rand((1, lq, h, d), device, seed=430 + 4 * i),
+            _rand((1, lq, h, d), device, seed=431 + 4 * i),
+            _rand((1, lq, h, d), device, seed=432 + 4 * i),
+            _rand((2, 1, c + lq, h, d), device, seed=433 + 4 * i)) for i in range(3)]
+
+    def call(i):
+        q, k, v, cache = ins[i]
+        return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+
+    refs = [_paired(lambda i=i: call(i), MERGE_KERNEL, 3) for i in range(3)]
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, 3), _lib.tuning(_lib.TUNE_ATTN_PMERGE, IN_KERNEL):
+        for splits in (3, 2, 5, 3):
+            with _lib.tuning(_lib.TUNE_ATTN_SPLITS, splits):
+                for i in range(3):
+                    got = call(i)
+                    torch.cuda.synchronize()
+                    if splits == 3:
+                        assert torch.equal(got, refs[i]), f"repeat splits={splits} input {i}"
+        with _lib.tuning(_lib.TUNE_ATTN_SPLITS, 3):
+            out = {}
+            graph = harness.capture(lambda: out.__setitem__("o", call(0)))
+            for rep in range(3):
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out["o"], refs[0]), f"graph replay {rep}"
+                eager = call(1)
+                torch.cuda.synchronize()
+                assert torch.equal(eager, refs[1]), f"eager call after replay {rep}"
