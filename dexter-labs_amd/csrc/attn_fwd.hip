@@ -1195,6 +1195,156 @@ __device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coo
   A::template store_rows<kAux>(ro, ro_bytes, nrows, area, r0, lane);
 }
 
+// Merge state of each work-item group (arrival and finish counters, chunk
+// claims), indexed by the group's first partial, in a region of fixed size at
+// the start of every attention workspace, so that no plan's partials ever
+// overlap another plan's state. Zero before a launch, zero after it.
+constexpr int kCounterStride = 16;           // ints per group state (arrivals, finished, claims)
+constexpr int kCounterSlots = 4096;          // partials a launch that merges in-kernel may have
+constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
+// Key splits of a work-item group merged in the kernel itself (paired and
+// dual-stream kernels), with no merge launch: every split stores its partial at device scope
+// (kScDevice), waits until the stores have completed and arrives on the
+// group's 64-bit counter (the arrival count in the low word, the arrivals from
+// XCD x in the nibble at bit 32 + 4 x); the split that brings the count to
+// n_splits resets the counter and merges all the group's partials into the
+// output, and the others are done. No workgroup ever waits for another, so
+// the order and placement in which the splits run do not matter. When every
+// split ran on the merging workgroup's XCD, the partials are read from that
+// XCD's L2 (kScXcd), else from memory (kScDevice). Groups of more than
+// kPMergeSplits splits take the separate merge kernel instead.
+constexpr int kPMergeSplits = 8;
+// Cache policy of loads of data that workgroups of this XCD stored (sc0):
+// past this CU's L1 to the XCD's L2, which holds every such store.
+constexpr int kScXcd = 1;
+
+// The merge, by the last split: thread t < nrows turns row t's records into
+// the split weights (into LDS) while every thread's loads of its units (row,
+// 8 dims: 16 bytes) of the first splits are in flight; then each thread adds
+// the splits' terms in split order, two splits per batch of loads, with the
+// merge kernel's arithmetic (merge_weights, merge_add2). BM: rows per work
+// item; NT: threads of the workgroup; SB: splits per batch of loads (UPT SB
+// 16-byte values per thread in flight); kAux: cache policy of the loads.
+template <int D, typename T, int BM, int NT, int SB, int kAux>
+__device__ __forceinline__ void merge_split_group(const AttnArgs& a, const Coord& it, int q0,
+                                                  int nrows, uint16_t* smem) {
+  constexpr int CR = D / 8;          // 16-byte units per row
+  constexpr int UPT = BM * CR / NT;  // units per thread
+  static_assert(BM * CR % NT == 0 && BM <= NT, "units deal evenly; a thread per row");
+  static_assert(kPMergeSplits % SB == 0, "whole batches");
+  const int t = int(threadIdx.x);
+  const int S = it.n_splits;
+  const uint32_t rows = uint32_t(a.bm);
+  // Bounded by the group's S partials: loads of splits s >= S return zeros.
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + it.pbase * a.bm * 4, (short)0, int(uint32_t(S) * rows * 16), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rval = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o + it.pbase * a.bm * D, (short)0, int(uint32_t(S) * rows * D * 2), kBufWord3);
+  float* const lc = reinterpret_cast<float*>(smem);                   // [row][kPMergeSplits]
+  int* const le = reinterpret_cast<int*>(lc + BM * kPMergeSplits);  // [row] exponent E
+
+  f32x4 ml[kPMergeSplits];
+  {
+    const uint32_t base = t < nrows ? uint32_t(t) * 16 : 0x80000000u;  // past every bound
+#pragma unroll
+    for (int s = 0; s < kPMergeSplits; ++s)
+      ml[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rrec, base + uint32_t(s) * rows * 16, 0, kAux));
+  }
+  u32x4 v[UPT][SB];
+  auto load_batch = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      const int u = t + NT * k, r = u / CR, ch = u % CR;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const uint32_t off = r < nrows ? (uint32_t(s0 + j) * rows + uint32_t(r)) * (D * 2) +
+                                             uint32_t(ch) * 16
+                                       : 0x80000000u;  // past every bound: zeros
+        v[k][j] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rval, off, 0, kAux));
+      }
+    }
+  };
+  load_batch(0);
+  {
+    float c[kPMergeSplits];
+    const int emax = merge_weights(ml, S, c);
+    if (t < nrows) {
+#pragma unroll
+      for (int s = 0; s < kPMergeSplits; ++s) lc[t * kPMergeSplits + s] = c[s];
+      le[t] = emax;
+    }
+  }
+  __syncthreads();
+  float acc[UPT][8];
+#pragma unroll
+  for (int k = 0; k < UPT; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
+  for (int s0 = 0; s0 < S; s0 += SB) {
+    if (s0 > 0) load_batch(s0);
+#pragma unroll
+    for (int k = 0; k < UPT; ++k) {
+      const int r = (t + NT * k) / CR;
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const float cs = lc[r * kPMergeSplits + s0 + j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) merge_add2(acc[k][2 * e], acc[k][2 * e + 1], cs, v[k][j][e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < UPT; ++k) {
+    const int u = t + NT * k, r = u / CR, ch = u % CR;
+    if (r < nrows) {
+      const int emax = le[r];
+      u32x4 packed;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        packed[e] = Mfma<T>::pack(__builtin_ldexpf(acc[k][2 * e], emax),
+                                  __builtin_ldexpf(acc[k][2 * e + 1], emax));
+      uint16_t* op = a.out + it.b * a.o_sb + int64_t(q0 + r) * a.o_sl + it.h * a.o_sh + ch * 8;
+      *reinterpret_cast<u32x4*>(op) = packed;
+    }
+  }
+}
+
+// Arrival of a split work item whose partial rows are being stored with
+// kScDevice (merge_split_group): every wave of the workgroup calls it, once
+// its own stores are issued. Uses the first BM (kPMergeSplits + 1) + 1 words
+// of the LDS, which must be idle.
+template <int D, typename T, int BM, int NT, int SB>
+__device__ __forceinline__ void arrive_split_group(const AttnArgs& a, const Coord& it, int q0,
+                                                   uint16_t* smem) {
+  static_assert(kPMergeSplits < 16, "an XCD's arrivals fit its nibble");
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed at device scope
+  __syncthreads();
+  int* const last = reinterpret_cast<int*>(smem) + BM * (kPMergeSplits + 1);  // past the weights
+  if (threadIdx.x == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+    uint64_t* const cnt = reinterpret_cast<uint64_t*>(a.counters + it.pbase * kCounterStride);
+    const uint64_t mine = 1ull | (1ull << (32 + 4 * xcc));
+    const uint64_t v =
+        __hip_atomic_fetch_add(cnt, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    const uint64_t n = uint64_t(it.n_splits);
+    int state = 0;  // 0: not the last; 1: the last, every split on this XCD; 2: the last
+    if ((v & 0xffffffffull) == n) {
+      state = (v >> 32) == (n << (4 * xcc)) ? 1 : 2;
+      __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *last = state;
+  }
+  __syncthreads();
+  const int state = *last;
+  if (state == 0) return;
+  const int nrows = min(BM, a.Lq - q0);
+  if (state == 1) merge_split_group<D, T, BM, NT, SB, kScXcd>(a, it, q0, nrows, smem);
+  else merge_split_group<D, T, BM, NT, SB, kScDevice>(a, it, q0, nrows, smem);
+}
+
 template <int D, typename T, int NS>
 __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) {
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
@@ -1421,32 +1571,47 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
               f32x4{acc[d][4 * q], acc[d][4 * q + 1], acc[d][4 * q + 2], acc[d][4 * q + 3]};
     }
     __syncthreads();
-    if (stream == 1) return;
-    const f32x4 h = x[ltid];
-    const float m1 = h[0], l1 = h[1];
-    const float mm = fmaxf(mref, m1);
-    const float base = mm == -INFINITY ? 0.f : mm;
-    const float w0 = fast_exp2(mref - base), w1 = fast_exp2(m1 - base);
-    sm.l = sm.l * w0 + l1 * w1;
+    if (stream == 1) {
+      // Done, unless the workgroup takes part in an in-launch merge (below).
+      if (a.counters == nullptr || it.n_splits == 1) return;
+    } else {
+      const f32x4 h = x[ltid];
+      const float m1 = h[0], l1 = h[1];
+      const float mm = fmaxf(mref, m1);
+      const float base = mm == -INFINITY ? 0.f : mm;
+      const float w0 = fast_exp2(mref - base), w1 = fast_exp2(m1 - base);
+      sm.l = sm.l * w0 + l1 * w1;
 #pragma unroll
-    for (int d = 0; d < DT; ++d)
+      for (int d = 0; d < DT; ++d)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 v = x[(1 + 4 * d + q) * LANES + ltid];
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = x[(1 + 4 * d + q) * LANES + ltid];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[d][4 * q + e] = acc[d][4 * q + e] * w0 + v[e] * w1;
-      }
-    mref = mm;
+          for (int e = 0; e < 4; ++e) acc[d][4 * q + e] = acc[d][4 * q + e] * w0 + v[e] * w1;
+        }
+      mref = mm;
+    }
   }
 
   const float l_tot = xor32_sum(sm.l);
-  if (!wave_active) return;
   // Result rows through the LDS, now free: the tile buffers of stream 1 (past
   // the hand-over area) or, with one stream, the tile buffers, whose last
   // reads and DMA pieces ended at the loop's last barrier.
-  const uint32_t smem_base = lds_addr(smem);
-  store_result_staged<D, T>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref,
-                            smem_base + (NS == 2 ? Lds<D>::bytes : 0));
+  const uint32_t area = lds_addr(smem) + (NS == 2 ? Lds<D>::bytes : 0);
+  if (a.counters == nullptr || it.n_splits == 1) {
+    if (!wave_active) return;
+    store_result_staged<D, T>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref, area);
+    return;
+  }
+  // Split, merged in this launch: stream 0 stores the partial, then every
+  // wave arrives (arrive_split_group); the last split of the group merges.
+  if (wave_active && stream == 0)
+    store_result_staged<D, T, kScDevice>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref,
+                                         area);
+  static_assert((kBM * (kPMergeSplits + 1) + 1) * 4 <= (NS == 2 ? Lds<D>::bytes : 0) ||
+                    NS == 1,
+                "merge scratch below the row area");
+  arrive_split_group<D, T, kBM, 64 * kNW * NS, 2>(a, it, q0, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1633,122 +1798,6 @@ __device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32
   }
 }
 
-// Merge state of each work-item group (arrival and finish counters, chunk
-// claims), indexed by the group's first partial, in a region of fixed size at
-// the start of every attention workspace, so that no plan's partials ever
-// overlap another plan's state. Zero before a launch, zero after it.
-constexpr int kCounterStride = 16;           // ints per group state (arrivals, finished, claims)
-constexpr int kCounterSlots = 4096;          // partials a launch that merges in-kernel may have
-constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
-// Key splits of a paired-kernel work-item group merged in the kernel itself,
-// with no merge launch: every split stores its partial at device scope
-// (kScDevice), waits until the stores have completed and arrives on the
-// group's 64-bit counter (the arrival count in the low word, the arrivals from
-// XCD x in the nibble at bit 32 + 4 x); the split that brings the count to
-// n_splits resets the counter and merges all the group's partials into the
-// output, and the others are done. No workgroup ever waits for another, so
-// the order and placement in which the splits run do not matter. When every
-// split ran on the merging workgroup's XCD, the partials are read from that
-// XCD's L2 (kScXcd), else from memory (kScDevice). Groups of more than
-// kPMergeSplits splits take the separate merge kernel instead.
-constexpr int kPMergeSplits = 8;
-// Cache policy of loads of data that workgroups of this XCD stored (sc0):
-// past this CU's L1 to the XCD's L2, which holds every such store.
-constexpr int kScXcd = 1;
-
-// The merge, by the last split: thread t < nrows turns row t's records into
-// the split weights (into LDS) while every thread's loads of its units (row,
-// 8 dims: 16 bytes) of the first splits are in flight; then each thread adds
-// the splits' terms in split order, two splits per batch of loads, with the
-// merge kernel's arithmetic (merge_weights, merge_add2). kAux: cache policy
-// of the loads.
-template <int D, typename T, int kAux>
-__device__ __forceinline__ void pair_merge_group(const AttnArgs& a, const Coord& it, int q0,
-                                                 int nrows, uint16_t* smem) {
-  constexpr int CR = D / 8;               // 16-byte units per row
-  constexpr int NT = 64 * kPairWaves;
-  constexpr int UPT = kBMPair * CR / NT;  // units per thread
-  constexpr int SB = 2;                   // splits per batch of loads
-  static_assert(kBMPair * CR % NT == 0 && kBMPair <= NT, "units deal evenly; a thread per row");
-  static_assert(kPMergeSplits % SB == 0, "whole batches");
-  const int t = int(threadIdx.x);
-  const int S = it.n_splits;
-  const uint32_t rows = uint32_t(a.bm);
-  // Bounded by the group's S partials: loads of splits s >= S return zeros.
-  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
-      a.ws_ml + it.pbase * a.bm * 4, (short)0, int(uint32_t(S) * rows * 16), kBufWord3);
-  const __amdgpu_buffer_rsrc_t rval = __builtin_amdgcn_make_buffer_rsrc(
-      a.ws_o + it.pbase * a.bm * D, (short)0, int(uint32_t(S) * rows * D * 2), kBufWord3);
-  float* const lc = reinterpret_cast<float*>(smem);                   // [row][kPMergeSplits]
-  int* const le = reinterpret_cast<int*>(lc + kBMPair * kPMergeSplits);  // [row] exponent E
-
-  f32x4 ml[kPMergeSplits];
-  {
-    const uint32_t base = t < nrows ? uint32_t(t) * 16 : 0x80000000u;  // past every bound
-#pragma unroll
-    for (int s = 0; s < kPMergeSplits; ++s)
-      ml[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rrec, base + uint32_t(s) * rows * 16, 0, kAux));
-  }
-  u32x4 v[UPT][SB];
-  auto load_batch = [&](int s0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < UPT; ++k) {
-      const int u = t + NT * k, r = u / CR, ch = u % CR;
-#pragma unroll
-      for (int j = 0; j < SB; ++j) {
-        const uint32_t off = r < nrows ? (uint32_t(s0 + j) * rows + uint32_t(r)) * (D * 2) +
-                                             uint32_t(ch) * 16
-                                       : 0x80000000u;  // past every bound: zeros
-        v[k][j] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rval, off, 0, kAux));
-      }
-    }
-  };
-  load_batch(0);
-  {
-    float c[kPMergeSplits];
-    const int emax = merge_weights(ml, S, c);
-    if (t < nrows) {
-#pragma unroll
-      for (int s = 0; s < kPMergeSplits; ++s) lc[t * kPMergeSplits + s] = c[s];
-      le[t] = emax;
-    }
-  }
-  __syncthreads();
-  float acc[UPT][8];
-#pragma unroll
-  for (int k = 0; k < UPT; ++k)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
-  for (int s0 = 0; s0 < S; s0 += SB) {
-    if (s0 > 0) load_batch(s0);
-#pragma unroll
-    for (int k = 0; k < UPT; ++k) {
-      const int r = (t + NT * k) / CR;
-#pragma unroll
-      for (int j = 0; j < SB; ++j) {
-        const float cs = lc[r * kPMergeSplits + s0 + j];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) merge_add2(acc[k][2 * e], acc[k][2 * e + 1], cs, v[k][j][e]);
-      }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < UPT; ++k) {
-    const int u = t + NT * k, r = u / CR, ch = u % CR;
-    if (r < nrows) {
-      const int emax = le[r];
-      u32x4 packed;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        packed[e] = Mfma<T>::pack(__builtin_ldexpf(acc[k][2 * e], emax),
-                                  __builtin_ldexpf(acc[k][2 * e + 1], emax));
-      uint16_t* op = a.out + it.b * a.o_sb + int64_t(q0 + r) * a.o_sl + it.h * a.o_sh + ch * 8;
-      *reinterpret_cast<u32x4*>(op) = packed;
-    }
-  }
-}
 
 template <int D, typename T>
 __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs a) {
@@ -1961,38 +2010,14 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
     store_result_staged<D, T>(a, it, BM, q0, r0, g, lane, acc, l_tot, mref, area);
     return;
   }
-  // Split, merged in this launch (pair_merge_group): arrive once this
-  // workgroup's partial is stored; the last of the group merges.
+  // Split, merged in this launch (arrive_split_group): arrive once this
+  // workgroup's partial is stored; the last of the group merges, in the K/V
+  // stages (idle after the loop).
   if (wave_active)
     store_result_staged<D, T, kScDevice>(a, it, BM, q0, r0, g, lane, acc, l_tot, mref, area);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed at device scope
-  __syncthreads();
-  // The flag sits in the last word of the K/V stages (idle after the loop),
-  // clear of the merge's weights at the start of the LDS.
-  int* const last = reinterpret_cast<int*>(smem) + PairLds<D>::bytes / 4 - 1;
-  static_assert(kBMPair * (kPMergeSplits + 1) * 4 < PairLds<D>::bytes, "merge scratch fits");
-  static_assert(kPMergeSplits < 16, "an XCD's arrivals fit its nibble");
-  if (threadIdx.x == 0) {
-    uint32_t xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
-    uint64_t* const cnt = reinterpret_cast<uint64_t*>(a.counters + it.pbase * kCounterStride);
-    const uint64_t mine = 1ull | (1ull << (32 + 4 * xcc));
-    const uint64_t v =
-        __hip_atomic_fetch_add(cnt, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
-    const uint64_t n = uint64_t(it.n_splits);
-    int state = 0;  // 0: not the last; 1: the last, every split on this XCD; 2: the last
-    if ((v & 0xffffffffull) == n) {
-      state = (v >> 32) == (n << (4 * xcc)) ? 1 : 2;
-      __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    *last = state;
-  }
-  __syncthreads();
-  const int state = *last;
-  if (state == 0) return;
-  const int nrows = min(BM, a.Lq - q0);
-  if (state == 1) pair_merge_group<D, T, kScXcd>(a, it, q0, nrows, smem);
-  else pair_merge_group<D, T, kScDevice>(a, it, q0, nrows, smem);
+  static_assert((BM * (kPMergeSplits + 1) + 1) * 4 <= PairLds<D>::bytes, "merge scratch fits");
+  // Two splits per batch: the K/V loop's registers leave room for no more.
+  arrive_split_group<D, T, BM, 64 * kPairWaves, 2>(a, it, q0, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -2770,7 +2795,7 @@ struct Plan {
   std::vector<int> seg_b, seg_splits, seg_cache, seg_base, comb_base;
   int64_t items, comb_blocks, partials;
   int64_t counter_bytes;     // arrival counters at the start of the workspace
-  bool pmerge;               // paired kernel: splits merged in the kernel (no merge launch)
+  bool pmerge;               // splits merged in the kernel (no merge launch)
   int64_t ws_bytes;
 };
 
@@ -2999,12 +3024,17 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   p.ws_bytes = has_partials
                    ? kCounterRegion + p.partials * p.prow * (D * 2 + 4 * int64_t(sizeof(float)))
                    : 0;
-  // The paired kernel merges its splits itself (pair_merge_group) when no
-  // group has more than kPMergeSplits and the counters cover every group.
+  // The paired kernel merges its splits itself (arrive_split_group) when no
+  // group has more than kPMergeSplits and the counters cover every group; the
+  // dual-stream kernel can too, but only when told to: at C1 (8 splits of 83
+  // rows) one workgroup's merge of 170 KB of partials took longer than the
+  // merge kernel, 14.7 vs 12.7 us per call.
   int most = p.uniform_splits;
   for (int sk : p.seg_splits) most = std::max(most, sk);
-  p.pmerge = p.kernel == kPaired && has_partials && most <= kPMergeSplits &&
-             p.partials <= kCounterSlots && tuning(DX_TUNE_ATTN_PMERGE) != 1;
+  const int pm = tuning(DX_TUNE_ATTN_PMERGE);
+  p.pmerge = (pm == 2 ? p.kernel == kPaired || p.kernel == kDual
+                      : pm == 0 && p.kernel == kPaired) &&
+             has_partials && most <= kPMergeSplits && p.partials <= kCounterSlots;
   if (p.pmerge) p.comb_blocks = 0;
   return p;
 }
@@ -3222,7 +3252,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   // Workspace: [counters][f16 partial values][fp32 records].
   char* ws = static_cast<char*>(workspace);
   // The merge state of kernels that merge their splits themselves: the
-  // decode kernel always, the paired kernel when planned so.
+  // decode kernel always, the paired and dual-stream kernels when planned so.
   a.counters = p.counter_bytes && (p.kernel == kDecode || p.pmerge)
                    ? reinterpret_cast<int32_t*>(ws)
                    : nullptr;

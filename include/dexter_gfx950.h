@@ -93,10 +93,12 @@ int dx_abi_version(void);
  *   DX_TUNE_ATTN_MERGE   one-launch decode merge: 1 through the L2 when the
  *                        splits share an XCD (the default), 2 at device
  *                        scope only (for tests)
- *   DX_TUNE_ATTN_PMERGE  paired prefill with key splits: 1 merges them in a
- *                        separate merge kernel, 2 in the prefill kernel (the
- *                        last split of each query tile to finish merges all
- *                        of its partials; the default)
+ *   DX_TUNE_ATTN_PMERGE  key splits of the paired and dual-stream kernels:
+ *                        1 merged by a separate merge kernel, 2 in the same
+ *                        launch (the last split of each query tile to finish
+ *                        merges all of its partials). Default: the paired
+ *                        kernel in the launch, the dual-stream kernel by the
+ *                        merge kernel
  * Returns DX_EINVAL for an unknown key or an out-of-range value.
  * No reference counterpart (the reference's tuning is Triton's autotuner).
  */

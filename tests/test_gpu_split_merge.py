@@ -1,10 +1,12 @@
-"""Key splits of the paired prefill kernel merged inside the kernel (MI355X).
+"""Key splits merged inside the attention kernel itself (MI355X): the paired
+prefill kernel and the dual-stream decode kernel.
 
 With key splits, each split of a (batch, head, query tile) group leaves a
-partial output; by default the split of the group that finishes last merges
-them all in the same launch (``DX_TUNE_ATTN_PMERGE`` 2), and the separate merge
-kernel (``DX_TUNE_ATTN_PMERGE`` 1) remains for groups of more than eight
-splits. Both merges add the splits' terms in the same order with the same
+partial output. Under ``DX_TUNE_ATTN_PMERGE`` 2 the split of the group that
+finishes last merges them all in the same launch (the paired kernel's default;
+the dual-stream kernel's only when forced), and under 1 the separate merge
+kernel does (the dual-stream kernel's default, and every kernel's for groups
+of more than eight splits). Both merges add the splits' terms in the same order with the same
 arithmetic, so their outputs must agree bit for bit; the merged result is also
 held to the north-star bar against the oracle
 (``python/dexter/ops/reference/attention.py:71-77``). The arrival counters
@@ -27,6 +29,8 @@ from _util import assert_parity
 pytestmark = pytest.mark.gpu
 
 IN_KERNEL, MERGE_KERNEL = 2, 1
+# DX_TUNE_ATTN_KERNEL values of the kernels that merge in the launch.
+KERNELS = [("paired", 3), ("dual", 2)]
 
 
 def _rand(shape, device, dtype=torch.bfloat16, seed=0):
@@ -40,8 +44,8 @@ def _oracle(q, k, v, cache, cache_len, bb=None):
         None if bb is None else bb.cpu(), None, False, keep_fp32=True)
 
 
-def _paired(fn, merge, splits=0):
-    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, 3), _lib.tuning(_lib.TUNE_ATTN_PMERGE, merge), \
+def _run(fn, kernel, merge, splits=0):
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, kernel), _lib.tuning(_lib.TUNE_ATTN_PMERGE, merge), \
             _lib.tuning(_lib.TUNE_ATTN_SPLITS, splits):
         out = fn()
     torch.cuda.synchronize()
@@ -57,10 +61,11 @@ SHAPES = [(300, 300, 700, 8, 128, torch.bfloat16), (145, 145, 900, 5, 128, torch
           (257, 257, 600, 3, 128, torch.float16)]
 
 
+@pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"q{s[0]}-c{s[2]}-h{s[3]}-d{s[4]}-{str(s[5])[6:]}"
                                                for s in SHAPES])
 @pytest.mark.parametrize("splits", [2, 3, 5, 8])
-def test_in_kernel_merge_matches_merge_kernel(device, built_lib, shape, splits):
+def test_in_kernel_merge_matches_merge_kernel(device, built_lib, kernel, shape, splits):
     lq, lk, c, h, d, dt = shape
     q = _rand((1, lq, h, d), device, dt, seed=400)
     k = _rand((1, lk, h, d), device, dt, seed=401)
@@ -70,20 +75,22 @@ def test_in_kernel_merge_matches_merge_kernel(device, built_lib, shape, splits):
     def call():
         return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
 
-    got = _paired(call, IN_KERNEL, splits)
-    ref = _paired(call, MERGE_KERNEL, splits)
-    assert torch.equal(got, ref), f"splits={splits}: in-kernel merge differs from the merge kernel"
+    got = _run(call, kernel[1], IN_KERNEL, splits)
+    ref = _run(call, kernel[1], MERGE_KERNEL, splits)
+    assert torch.equal(got, ref), f"{kernel[0]} splits={splits}: in-kernel merge differs"
     if dt == torch.bfloat16:
-        assert_parity(got, _oracle(q, k, v, cache, c), what=f"{shape} splits={splits}")
+        assert_parity(got, _oracle(q, k, v, cache, c), what=f"{kernel[0]} {shape} splits={splits}")
 
 
-def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib):
+@pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
+def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib, kernel):
     """No cache and no mask (cross-attention), then a block list over a cache."""
+    kern = kernel[1]
     q = _rand((2, 300, 4, 128), device, seed=410)
     k, v = _rand((2, 700, 4, 128), device, seed=411), _rand((2, 700, 4, 128), device, seed=412)
     for splits in (2, 4, 7):
-        got = _paired(lambda: ops.blockwise_causal_attention(q, k, v), IN_KERNEL, splits)
-        ref = _paired(lambda: ops.blockwise_causal_attention(q, k, v), MERGE_KERNEL, splits)
+        got = _run(lambda: ops.blockwise_causal_attention(q, k, v), kern, IN_KERNEL, splits)
+        ref = _run(lambda: ops.blockwise_causal_attention(q, k, v), kern, MERGE_KERNEL, splits)
         assert torch.equal(got, ref), f"cross splits={splits}"
         assert_parity(got, _oracle(q, k, v, None, 0), what=f"cross splits={splits}")
     cache = _rand((2, 2, 1000, 4, 128), device, seed=413)
@@ -94,14 +101,15 @@ def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib):
         return ops.blockwise_causal_attention(q, kn, vn, kv_cache=cache, cache_len=700,
                                               block_boundaries=bb)
 
-    got = _paired(blocks, IN_KERNEL, 3)
-    assert torch.equal(got, _paired(blocks, MERGE_KERNEL, 3)), "block list splits=3"
+    got = _run(blocks, kern, IN_KERNEL, 3)
+    assert torch.equal(got, _run(blocks, kern, MERGE_KERNEL, 3)), "block list splits=3"
     assert_parity(got, _oracle(q, kn, vn, cache, 700, bb), what="block list splits=3")
 
 
-def test_in_kernel_merge_ragged_batch(device, built_lib):
-    """The C4 ragged lengths on the paired kernel with the planner's splits
-    (several per long sequence, one for the short ones)."""
+@pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
+def test_in_kernel_merge_ragged_batch(device, built_lib, kernel):
+    """The C4 ragged lengths with the planner's splits (several per long
+    sequence, one for the short ones)."""
     lens = [0, 332, 1245, 3237]
     h, d = 8, 128
     q, k, v = (_rand((4, 99, h, d), device, seed=420 + i) for i in range(3))
@@ -112,15 +120,16 @@ def test_in_kernel_merge_ragged_batch(device, built_lib):
         return ops.blockwise_causal_attention_varlen(q, k, v, kv_cache=cache, cache_lens=lens,
                                                      block_boundaries=bb)
 
-    got = _paired(call, IN_KERNEL)
-    assert torch.equal(got, _paired(call, MERGE_KERNEL)), "ragged batch"
+    got = _run(call, kernel[1], IN_KERNEL)
+    assert torch.equal(got, _run(call, kernel[1], MERGE_KERNEL)), f"{kernel[0]} ragged batch"
     for i, c in enumerate(lens):
         assert_parity(got[i:i + 1], _oracle(q[i:i + 1], k[i:i + 1], v[i:i + 1],
                                             cache[:, i:i + 1], c, bb), what=f"seq {i}")
 
 
+@pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
 @pytest.mark.parametrize("h", [8, 5])
-def test_in_kernel_merge_repeats_and_graph_replays(device, built_lib, h):
+def test_in_kernel_merge_repeats_and_graph_replays(device, built_lib, kernel, h):
     """Calls of different split counts one after another on the same workspace,
     then a captured call replayed with eager calls in between: every result
     equals the merge kernel's (a counter left nonzero would skip or repeat a
@@ -136,8 +145,9 @@ def test_in_kernel_merge_repeats_and_graph_replays(device, built_lib, h):
         q, k, v, cache = ins[i]
         return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
 
-    refs = [_paired(lambda i=i: call(i), MERGE_KERNEL, 3) for i in range(3)]
-    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, 3), _lib.tuning(_lib.TUNE_ATTN_PMERGE, IN_KERNEL):
+    refs = [_run(lambda i=i: call(i), kernel[1], MERGE_KERNEL, 3) for i in range(3)]
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, kernel[1]), \
+            _lib.tuning(_lib.TUNE_ATTN_PMERGE, IN_KERNEL):
         for splits in (3, 2, 5, 3):
             with _lib.tuning(_lib.TUNE_ATTN_SPLITS, splits):
                 for i in range(3):
