@@ -2948,8 +2948,10 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     } else {
       // Decode-shaped calls take the dual-stream kernel (128-query items, one
       // workgroup per CU): a uniform call when its 128-query groups fill at
-      // most half the CUs, a ragged batch when splits in proportion to length
-      // leave <= 8 tiles per split. Everything else takes paired groups.
+      // most half the CUs, a ragged batch when its chunks fit one 128-query
+      // item (all eight waves on the chunk's rows; C4: 27.6 vs 28.3 us on
+      // paired groups) or splits in proportion to length leave <= 8 tiles per
+      // split. Everything else takes paired groups.
       const int64_t g128 = units * cdiv(Lq, kBM);
       bool dual;
       if (nseg == 1) {
@@ -2962,7 +2964,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
           s = std::max<int64_t>(1, std::min<int64_t>({s, kMaxSplits, std::max<int64_t>(tiles[k], 1)}));
           worst = std::max(worst, cdiv(tiles[k], s));
         }
-        dual = worst <= 8;
+        dual = worst <= 8 || Lq <= kBM;
       }
       p.kernel = dual ? kDual : kPaired;
     }
@@ -3025,15 +3027,18 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
                    ? kCounterRegion + p.partials * p.prow * (D * 2 + 4 * int64_t(sizeof(float)))
                    : 0;
   // The paired kernel merges its splits itself (arrive_split_group) when no
-  // group has more than kPMergeSplits and the counters cover every group; the
-  // dual-stream kernel can too, but only when told to: at C1 (8 splits of 83
-  // rows) one workgroup's merge of 170 KB of partials took longer than the
-  // merge kernel, 14.7 vs 12.7 us per call.
+  // group has more than kPMergeSplits and the counters cover every group; so
+  // does the dual-stream kernel on ragged batches, whose groups end at
+  // different times, so that a group's merge overlaps other groups' tiles
+  // (C4: 27.6 vs 28.7 us). On a uniform call every split ends together and
+  // the merge lies on the critical path: at C1 (8 splits of 83 rows) one
+  // workgroup's merge of 170 KB of partials took longer than the merge kernel,
+  // 14.7 vs 12.7 us per call.
   int most = p.uniform_splits;
   for (int sk : p.seg_splits) most = std::max(most, sk);
   const int pm = tuning(DX_TUNE_ATTN_PMERGE);
-  p.pmerge = (pm == 2 ? p.kernel == kPaired || p.kernel == kDual
-                      : pm == 0 && p.kernel == kPaired) &&
+  const bool in_launch = p.kernel == kPaired || (p.kernel == kDual && p.n_seg > 0);
+  p.pmerge = (pm == 2 ? p.kernel == kPaired || p.kernel == kDual : pm == 0 && in_launch) &&
              has_partials && most <= kPMergeSplits && p.partials <= kCounterSlots;
   if (p.pmerge) p.comb_blocks = 0;
   return p;

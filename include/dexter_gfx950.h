@@ -96,9 +96,9 @@ int dx_abi_version(void);
  *   DX_TUNE_ATTN_PMERGE  key splits of the paired and dual-stream kernels:
  *                        1 merged by a separate merge kernel, 2 in the same
  *                        launch (the last split of each query tile to finish
- *                        merges all of its partials). Default: the paired
- *                        kernel in the launch, the dual-stream kernel by the
- *                        merge kernel
+ *                        merges all of its partials). Default: in the
+ *                        launch for the paired kernel and for ragged batches
+ *                        on the dual-stream kernel, else the merge kernel
  * Returns DX_EINVAL for an unknown key or an out-of-range value.
  * No reference counterpart (the reference's tuning is Triton's autotuner).
  */
