@@ -165,3 +165,26 @@ def test_in_kernel_merge_repeats_and_graph_replays(device, built_lib, kernel, h)
                 eager = call(1)
                 torch.cuda.synchronize()
                 assert torch.equal(eager, refs[1]), f"eager call after replay {rep}"
+
+
+@pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
+@pytest.mark.parametrize("heads", [(8, 2), (6, 3), (16, 4)])
+def test_in_kernel_merge_grouped_query(device, built_lib, kernel, heads):
+    """Grouped-query K/V (fewer K/V heads than query heads): the work-item map
+    keeps the query heads of a K/V head together, and each query head's splits
+    still merge in the launch, from the L2 or from memory."""
+    h, hkv = heads
+    lq, c = 200, 600
+    q = _rand((1, lq, h, 128), device, seed=440)
+    k = _rand((1, lq, hkv, 128), device, seed=441)
+    v = _rand((1, lq, hkv, 128), device, seed=442)
+    cache = _rand((2, 1, c + lq, hkv, 128), device, seed=443)
+
+    def call():
+        return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
+
+    for splits in (2, 5):
+        got = _run(call, kernel[1], IN_KERNEL, splits)
+        assert torch.equal(got, _run(call, kernel[1], MERGE_KERNEL, splits)), (
+            f"{kernel[0]} GQA {h}/{hkv} splits={splits}")
+        assert_parity(got, _oracle(q, k, v, cache, c), what=f"{kernel[0]} GQA {h}/{hkv}")
