@@ -1203,9 +1203,9 @@ constexpr int kCounterStride = 16;           // ints per group state (arrivals, 
 constexpr int kCounterSlots = 4096;          // partials a launch that merges in-kernel may have
 constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
 // Key splits of a work-item group merged in the kernel itself (paired and
-// dual-stream kernels), with no merge launch: every split stores its partial at device scope
-// (kScDevice), waits until the stores have completed and arrives on the
-// group's 64-bit counter (the arrival count in the low word, the arrivals from
+// dual-stream kernels), with no merge launch: every split stores its partial
+// at device scope (kScDevice), waits until the stores have completed and
+// arrives on the group's 64-bit counter (the arrival count in the low word, the arrivals from
 // XCD x in the nibble at bit 32 + 4 x); the split that brings the count to
 // n_splits resets the counter and merges all the group's partials into the
 // output, and the others are done. No workgroup ever waits for another, so
@@ -1221,7 +1221,7 @@ constexpr int kScXcd = 1;
 // The merge, by the last split: thread t < nrows turns row t's records into
 // the split weights (into LDS) while every thread's loads of its units (row,
 // 8 dims: 16 bytes) of the first splits are in flight; then each thread adds
-// the splits' terms in split order, two splits per batch of loads, with the
+// the splits' terms in split order, SB splits per batch of loads, with the
 // merge kernel's arithmetic (merge_weights, merge_add2). BM: rows per work
 // item; NT: threads of the workgroup; SB: splits per batch of loads (UPT SB
 // 16-byte values per thread in flight); kAux: cache policy of the loads.
