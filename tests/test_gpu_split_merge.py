@@ -107,11 +107,13 @@ def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib, kernel):
 
 
 @pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
-def test_in_kernel_merge_ragged_batch(device, built_lib, kernel):
+@pytest.mark.parametrize("h", [8, 5])
+def test_in_kernel_merge_ragged_batch(device, built_lib, kernel, h):
     """The C4 ragged lengths with the planner's splits (several per long
-    sequence, one for the short ones)."""
+    sequence, one for the short ones); 5 heads spread each group's splits over
+    several XCDs (merged from memory)."""
     lens = [0, 332, 1245, 3237]
-    h, d = 8, 128
+    d = 128
     q, k, v = (_rand((4, 99, h, d), device, seed=420 + i) for i in range(3))
     cache = _rand((2, 4, max(lens), h, d), device, seed=423)
     bb = torch.tensor([0, 83], dtype=torch.int32, device=device)
@@ -121,7 +123,7 @@ def test_in_kernel_merge_ragged_batch(device, built_lib, kernel):
                                                      block_boundaries=bb)
 
     got = _run(call, kernel[1], IN_KERNEL)
-    assert torch.equal(got, _run(call, kernel[1], MERGE_KERNEL)), f"{kernel[0]} ragged batch"
+    assert torch.equal(got, _run(call, kernel[1], MERGE_KERNEL)), f"{kernel[0]} ragged h={h}"
     for i, c in enumerate(lens):
         assert_parity(got[i:i + 1], _oracle(q[i:i + 1], k[i:i + 1], v[i:i + 1],
                                             cache[:, i:i + 1], c, bb), what=f"seq {i}")
