@@ -139,3 +139,26 @@ def test_noalloc_refuses_a_call_beyond_its_scratch_before_any_launch(built_lib):
     assert need > (64 << 20)
     assert rc == _lib.DX_EWORKSPACE
     assert "static scratch" in lib.dx_last_error().decode()
+
+
+def test_planner_choices_at_the_measured_shapes(built_lib):
+    """The launch plans at the benchmark shapes, read back through the workspace
+    size (256 KiB of arrival counters, then per partial `rows` f16 values of D
+    and a 16-byte record per row). Each split count was chosen by measurement:
+    C1 8 splits of 128-row items, C3 3 splits of 256-row items, the C4 ragged
+    batch 1/1/2/6 by length, cross-attention onto 257 image keys 5 splits of one
+    tile and onto 512 text keys 4 of two; C2 (768 items) has none. Runs without
+    a GPU, where the planner assumes MI355X's 256 CUs."""
+    lib = _lib.load()
+    counters, d = 256 << 10, 128
+
+    def ws(partials, rows):
+        return counters + partials * rows * (2 * d + 16)
+
+    assert lib.dx_attention_workspace_bytes(1, 83, 83, 24, d, 1245, None) == ws(24 * 8, 128)
+    assert lib.dx_attention_workspace_bytes(1, 8192, 8192, 24, d, 0, None) == 0
+    assert lib.dx_attention_workspace_bytes(1, 913, 913, 40, d, 7304, None) == ws(40 * 4 * 3, 256)
+    lens = (ctypes.c_int64 * 4)(0, 332, 1245, 3237)
+    assert lib.dx_attention_workspace_bytes(4, 99, 99, 24, d, 0, lens) == ws(24 * (1 + 1 + 2 + 6), 128)
+    assert lib.dx_attention_workspace_bytes(1, 83, 257, 24, d, 0, None) == ws(24 * 5, 128)
+    assert lib.dx_attention_workspace_bytes(1, 83, 512, 24, d, 0, None) == ws(24 * 4, 128)
