@@ -1715,15 +1715,19 @@ template <int D, int NST = 3> struct PairAddr {
 // ahead of the MFMAs that consume it; the sched_group_barrier sequence keeps
 // the compiler from moving the reads back next to their MFMAs (which exposes
 // the LDS latency once per batch) or hoisting them all (which costs
-// registers).
-template <int D, typename T, int KST, int VST>
+// registers). kParts: kPhaseBoth, or kPhaseS for a work item's first step,
+// whose PV would multiply P = 0 (S alone, no packing: l and acc unchanged).
+constexpr int kPhaseS = 1, kPhaseBoth = 3;
+template <int D, typename T, int KST, int VST, int kParts = kPhaseBoth>
 __device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32x16 (&pf)[2],
                                                 float& l, f32x16 (&acc)[D / 32],
                                                 const u32x4 (&qr)[D / 16], f32x16 (&sc)[2]) {
   using L = PairLds<D>;
+  static_assert(kParts == kPhaseS || kParts == kPhaseBoth, "S alone, or S and PV");
+  constexpr bool kPV = kParts == kPhaseBoth;
   constexpr int KS = D / 16, DT = D / 32, RB = 2 * D;
-  constexpr int NQ = 2 * KS;      // S MFMAs: (half i % 2, k-step i / 2): two interleaved chains
-  constexpr int NP = 4 * DT;      // PV MFMAs: (key step u = i / DT, dims tile d = i % DT)
+  constexpr int NQ = 2 * KS;            // S MFMAs: (half i % 2, k-step i / 2): two interleaved chains
+  constexpr int NP = kPV ? 4 * DT : 0;  // PV MFMAs: (key step u = i / DT, dims tile d = i % DT)
   constexpr int NA = NQ + NP;
   constexpr int B = 2;            // MFMAs per batch; each batch's reads go out one batch early
   constexpr int NQB = NQ / B, NPB = NP / B;
@@ -1748,7 +1752,14 @@ __device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32
   // pk[u][e]: keys 8 (u % 2) + 2 e, +1 of half u / 2 (MFMA B-operand order).
   u32x4 pk[4];
   float part[2] = {0.f, 0.f};  // same pairing as the other kernels: identical sums
-  constexpr int PPB = 16 / NQB;   // packed pairs per S batch
+  constexpr int PPB = 16 / NQB;  // packed pairs per S batch
+  auto pack = [&](int w) __attribute__((always_inline)) {
+    const int u = w / 4, e = w % 4;
+    const uint32_t pp = Mfma<T>::pack(pf[u / 2][8 * (u % 2) + 2 * e],
+                                      pf[u / 2][8 * (u % 2) + 2 * e + 1]);
+    pk[u][e] = pp;
+    part[e & 1] = Mfma<T>::sum2(pp, part[e & 1]);
+  };
   sc[0] = f32x16{};
   sc[1] = f32x16{};
   u32x4 fr[2][B];
@@ -1770,18 +1781,12 @@ __device__ __forceinline__ void pair_mfma_phase(const PairAddr<D>& ad, const f32
         acc[q % DT] = Mfma<T>::run(fr[b & 1][i], pk[q / DT], acc[q % DT]);
       }
     }
-    if (b < NQB) {
+    if (kPV && b < NQB) {
 #pragma unroll
-      for (int x = 0; x < PPB; ++x) {
-        const int w = b * PPB + x, u = w / 4, e = w % 4;
-        const uint32_t pp = Mfma<T>::pack(pf[u / 2][8 * (u % 2) + 2 * e],
-                                          pf[u / 2][8 * (u % 2) + 2 * e + 1]);
-        pk[u][e] = pp;
-        part[e & 1] = Mfma<T>::sum2(pp, part[e & 1]);
-      }
+      for (int x = 0; x < PPB; ++x) pack(b * PPB + x);
     }
   }
-  l += part[0] + part[1];
+  if (kPV) l += part[0] + part[1];
   // Schedule: batch b's MFMAs after the reads of batch b + 1 (two LDS reads
   // per PV MFMA, one per S MFMA).
   __builtin_amdgcn_sched_group_barrier(sg::kDsRead, B, 0);
@@ -1904,19 +1909,23 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
     constexpr int R = decltype(rc)::value;  // j mod 3
     dma.issue(m, src, smem_b, t_begin, nt, j + 2, j + 1, (R + 2) % 3, (R + 1) % 3, wid);
   };
-  // One straight-line body for every MFMA phase: the first (j = 0) runs PV
-  // with P = 0 (acc unchanged), the last (j = nt) computes an S that is never
-  // used, from a stale but in-bounds K buffer. One extra tile of MFMAs per
-  // work item, against a single register allocation for the phase. The wave
-  // in its MFMA phase issues ahead of its SIMD partner (raised priority): an
-  // MFMA it cannot issue idles the matrix pipe, while the partner's vector
-  // work fills whatever issue cycles are left.
+  // The first MFMA phase (j = 0) computes S only (its PV would multiply
+  // P = 0); every later one runs one straight-line body, so the last (j = nt)
+  // also computes an S that is never used, from a stale but in-bounds K
+  // buffer: a branch to a PV-only last phase inside the loop costs the loop
+  // its single register allocation (hundreds of spilled VGPRs). The wave in
+  // its MFMA phase issues ahead of its SIMD partner
+  // (raised priority): an MFMA it cannot issue idles the matrix pipe, while
+  // the partner's vector work fills whatever issue cycles are left.
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) pf[kt] = f32x16{};
-  auto mfma_phase = [&](auto rc) __attribute__((always_inline)) {
+  using Both = std::integral_constant<int, kPhaseBoth>;
+  using OnlyS = std::integral_constant<int, kPhaseS>;
+  auto mfma_phase = [&](auto rc, auto parts) __attribute__((always_inline)) {
     constexpr int R = decltype(rc)::value;  // j mod 3: K stage R, V stage R - 1
+    constexpr int P = decltype(parts)::value;
     __builtin_amdgcn_s_setprio(1);
-    if (wave_active) pair_mfma_phase<D, T, R, (R + 2) % 3>(ad, pf, sm.l, acc, qr, sc);
+    if (wave_active) pair_mfma_phase<D, T, R, (R + 2) % 3, P>(ad, pf, sm.l, acc, qr, sc);
     __builtin_amdgcn_s_setprio(0);
   };
   static_assert(Dma::NP == 4 || Dma::NP == 2, "DMA slots are spread over the 32 exponentials");
@@ -1965,17 +1974,17 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
       if (j >= nt) break;
       valu_phase(j, S0{});
       end_phase(first_even);
-      mfma_phase(S1{});
+      mfma_phase(S1{}, Both{});
       end_phase(!first_even);
       if (++j >= nt) break;
       valu_phase(j, S1{});
       end_phase(first_even);
-      mfma_phase(S2{});
+      mfma_phase(S2{}, Both{});
       end_phase(!first_even);
       if (++j >= nt) break;
       valu_phase(j, S2{});
       end_phase(first_even);
-      mfma_phase(S0{});
+      mfma_phase(S0{}, Both{});
       end_phase(!first_even);
       ++j;
     }
@@ -1983,7 +1992,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   if (grp == 0) {
 #pragma unroll
     for (int m = 0; m < Dma::NP; ++m) send(-1, S2{}, m);
-    mfma_phase(S0{});        // p = -1
+    mfma_phase(S0{}, OnlyS{});  // p = -1
     end_phase(false);
     steps(true);             // p = 2j (VALU), 2j + 1 (MFMA)
     end_phase(true);         // p = 2 nt
@@ -1991,7 +2000,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
 #pragma unroll
     for (int m = 0; m < Dma::NP; ++m) send(-1, S2{}, m);
     end_phase(false);        // p = -1
-    mfma_phase(S0{});        // p = 0
+    mfma_phase(S0{}, OnlyS{});  // p = 0
     end_phase(true);
     steps(false);            // p = 2j + 1 (VALU), 2j + 2 (MFMA)
   }
