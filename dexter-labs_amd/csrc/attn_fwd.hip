@@ -635,12 +635,14 @@ template <int D> struct RowArea {
   // to the rows of a buffer with the given row stride; the wave's other rows
   // are not written (bounded by the row count, not by the buffer: a one-row
   // tensor may come with row stride 0).
-  // kAux: the stores' cache policy (0, or kScDevice: through to memory).
-  template <int kAux = 0>
+  // kAux: the stores' cache policy (0, or kScDevice: through to memory); NR:
+  // rows r0 .. r0 + NR - 1 (32: the wave's whole row range).
+  template <int kAux = 0, int NR = 32>
   __device__ __forceinline__ static void store_rows(__amdgpu_buffer_rsrc_t ro, int row_bytes,
                                                     int rows, uint32_t area, int r0, int lane) {
+    static_assert(NR % RPP == 0 && NR <= 32, "whole store instructions within a wave's rows");
 #pragma unroll
-    for (int i = 0; i < 32 / RPP; ++i) {
+    for (int i = 0; i < NR / RPP; ++i) {
       const int r = i * RPP + lane / CR, x = lane % CR;
       const u32x4 v = lds_read_b128_at(at(area, r0 + r, x));
       const uint32_t o = uint32_t(r) * uint32_t(row_bytes) + 16u * x;
@@ -1089,6 +1091,9 @@ __device__ __forceinline__ void store_result(const AttnArgs& a, const Coord& it,
 // selects, not branches, so every load is issued before any is used.
 template <int NMAX>
 __device__ __forceinline__ int merge_weights(const f32x4 (&ml)[NMAX], int n, float (&c)[NMAX]) {
+  // No fused multiply-adds: the merge kernel and the in-launch merges inline
+  // this into different code and must round alike.
+#pragma clang fp contract(off)
   float mmax = -INFINITY;
   int emax = INT_MIN;
 #pragma unroll
@@ -1115,8 +1120,8 @@ __device__ __forceinline__ int merge_weights(const f32x4 (&ml)[NMAX], int n, flo
 // adds the splits' terms in split order, so the separate merge kernel and the
 // prefill kernel's own merge round alike.
 __device__ __forceinline__ void merge_add2(float& a0, float& a1, float c, uint32_t o) {
-  a0 += c * to_f32(f16_t{uint16_t(o & 0xffffu)});
-  a1 += c * to_f32(f16_t{uint16_t(o >> 16)});
+  a0 = __builtin_fmaf(c, to_f32(f16_t{uint16_t(o & 0xffffu)}), a0);
+  a1 = __builtin_fmaf(c, to_f32(f16_t{uint16_t(o >> 16)}), a1);
 }
 
 template <int NMAX>
@@ -1145,6 +1150,10 @@ __device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coo
                                                     int q0, int r0, int g, int lane,
                                                     const f32x16 (&acc)[D / 32], float l_tot,
                                                     float mref, uint32_t area) {
+  // Every product below is rounded to fp32 before its conversion: a multiply
+  // fused into the conversion (one rounding) would round differently, and
+  // inlined copies of this function must agree bit for bit.
+#pragma clang fp contract(off)
   constexpr int DT = D / 32;
   using A = RowArea<D>;
   const int row = r0 + (lane & 31);
@@ -1343,6 +1352,93 @@ __device__ __forceinline__ void arrive_split_group(const AttnArgs& a, const Coor
   const int nrows = min(BM, a.Lq - q0);
   if (state == 1) merge_split_group<D, T, BM, NT, SB, kScXcd>(a, it, q0, nrows, smem);
   else merge_split_group<D, T, BM, NT, SB, kScDevice>(a, it, q0, nrows, smem);
+}
+
+// The dual-stream kernel's results after its split hand-over: stream s holds
+// head_dim blocks [s DT / 2, (s + 1) DT / 2) of its wave's 32 rows (r0 ..)
+// and the whole row's (l_tot, mref). Both streams pack their blocks into the
+// row area at ``area``; after a workgroup barrier each stores 16 of the 32
+// rows, whole. A split partial takes one scale exponent per row
+// (partial_scale), from the row's largest |value| over both streams' blocks,
+// exchanged through ``ax`` (2 x 64 kNW floats of idle LDS). Every wave of the
+// workgroup calls it (the barriers); ``active``: the wave has rows below Lq.
+// The stream is a template parameter so that every block index is a constant
+// (a register array indexed at run time would live in scratch memory).
+template <int D, typename T, int stream, int kAux = 0>
+__device__ __forceinline__ void store_result_halves(const AttnArgs& a, const Coord& it, int q0,
+                                                    int r0, int g, int lane, int ltid,
+                                                    bool active,
+                                                    const f32x16 (&acc)[D / 32], float l_tot,
+                                                    float mref, uint32_t area, float* ax) {
+  // As in store_result_staged: each product rounded to fp32, then converted.
+#pragma clang fp contract(off)
+  constexpr int DT = D / 32, HB = DT / 2, LANES = 64 * kNW;
+  constexpr int d0 = stream * HB;
+  using A = RowArea<D>;
+  const int row = r0 + (lane & 31);
+  const int nrows = min(a.Lq - q0 - r0, 32);
+  float k;
+  int e = 0;
+  if (it.n_splits == 1) {
+    k = 1.0f / l_tot;
+  } else {
+    float amax = 0.f;
+#pragma unroll
+    for (int dd = 0; dd < HB; ++dd)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(acc[d0 + dd][r]));
+    amax = xor32_max(amax);  // the row's other half of each block (lanes l and l ^ 32)
+    ax[stream * LANES + ltid] = amax;
+    __syncthreads();
+    amax = fmaxf(amax, ax[(1 - stream) * LANES + ltid]);  // the other stream's blocks
+    const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    const float omax = amax * inv;
+    e = omax > 0.f && omax <= FLT_MAX ? __builtin_amdgcn_frexp_expf(omax) : 0;
+    k = __builtin_ldexpf(inv, -e);
+  }
+  if (active) {
+    // Dims 32 d + 8 r4 + 4 g .. + 3 of row ``row``: half g of chunk 4 d + r4.
+#pragma unroll
+    for (int dd = 0; dd < HB; ++dd)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = d0 + dd;
+        u32x2 w;
+        if (it.n_splits == 1) {
+          w[0] = Mfma<T>::pack(acc[d][4 * r4] * k, acc[d][4 * r4 + 1] * k);
+          w[1] = Mfma<T>::pack(acc[d][4 * r4 + 2] * k, acc[d][4 * r4 + 3] * k);
+        } else {
+          w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * k, acc[d][4 * r4 + 1] * k);
+          w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * k, acc[d][4 * r4 + 3] * k);
+        }
+        typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+        *reinterpret_cast<lds_u32x2*>(A::at(area, row, 4 * d + r4) + 8 * g) = w;
+      }
+    if (it.n_splits > 1 && stream == 0 && g == 0 && row - r0 < nrows) {
+      const int64_t pidx = it.pbase + it.split;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(u32x4, f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(e), 0.f}),
+          __builtin_amdgcn_make_buffer_rsrc(a.ws_ml + pidx * a.bm * 4, (short)0, a.bm * 16,
+                                            kBufWord3),
+          row * 16, 0, kAux);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's blocks are in LDS
+  __syncthreads();                     // both streams' blocks of every row
+  if (!active) return;
+  const int rs = r0 + 16 * stream;     // this stream stores rows rs .. rs + 15
+  const int nr = min(nrows - 16 * stream, 16);
+  __amdgpu_buffer_rsrc_t ro;
+  int ro_bytes;
+  if (it.n_splits == 1) {
+    ro_bytes = int(a.o_sl) * 2;
+    ro = make_rsrc(a.out + it.b * a.o_sb + int64_t(q0 + rs) * a.o_sl + it.h * a.o_sh,
+                   max(nr, 0), ro_bytes, D);
+  } else {
+    ro_bytes = D * 2;
+    ro = make_rsrc(a.ws_o + ((it.pbase + it.split) * a.bm + rs) * D, max(nr, 0), ro_bytes, D);
+  }
+  A::template store_rows<kAux, 16>(ro, ro_bytes, nr, area, rs, lane);
 }
 
 template <int D, typename T, int NS>
@@ -1551,67 +1647,85 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
 
   // The exponent reference of acc and l, in log2 units.
   float mref = sm.m == -INFINITY ? -INFINITY : sm.m * c;
-  if (NS == 2) {
-    // Stream 1 hands (mref, l, acc) to the same lane of stream 0 through LDS,
-    // in 16-byte vectors laid out [vector][lane]: consecutive lanes hit
-    // consecutive 16 bytes, and each lane moves 1 + 4 DT vectors instead of
-    // 2 + 16 DT single floats.
-    constexpr int LANES = 64 * kNW;
-    static_assert((1 + 4 * DT) * LANES * 16 <= 2 * 2 * Lds<D>::stage * 2,
-                  "the hand-off fits in the tile buffers");
-    f32x4* x = reinterpret_cast<f32x4*>(smem);
-    __syncthreads();  // all tile reads done: the LDS is free
-    if (stream == 1) {
-      x[ltid] = f32x4{mref, sm.l, 0.f, 0.f};
+  const bool merge_here = a.counters != nullptr && it.n_splits > 1;
+  if constexpr (NS == 2) {
+    // The streams swap halves through LDS: stream s keeps head_dim blocks
+    // [s DT / 2, (s + 1) DT / 2) and hands (mref, l) and its other blocks to
+    // the same lane of the other stream, in 16-byte vectors laid out
+    // [vector][lane] (consecutive lanes hit consecutive 16 bytes). Both then
+    // combine their blocks with the same weights, stream 0's terms first, and
+    // store them (store_result_halves): all eight waves share the combine and
+    // the stores. The stream enters as a constant, so every block index is
+    // static.
+    auto epilogue = [&](auto stream_c) __attribute__((always_inline)) {
+      constexpr int S = decltype(stream_c)::value;
+      constexpr int LANES = 64 * kNW, HB = DT / 2, NV = 1 + 4 * HB;
+      static_assert(2 * NV * LANES * 16 + 2 * LANES * 4 <= Lds<D>::bytes,
+                    "the hand-over and the max exchange lie below the row area");
+      f32x4* const x = reinterpret_cast<f32x4*>(smem);
+      f32x4* const hand = x + S * NV * LANES;
+      const f32x4* const got = x + (1 - S) * NV * LANES;
+      __syncthreads();  // all tile reads done: the LDS is free
+      hand[ltid] = f32x4{mref, sm.l, 0.f, 0.f};
 #pragma unroll
-      for (int d = 0; d < DT; ++d)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          x[(1 + 4 * d + q) * LANES + ltid] =
-              f32x4{acc[d][4 * q], acc[d][4 * q + 1], acc[d][4 * q + 2], acc[d][4 * q + 3]};
-    }
-    __syncthreads();
-    if (stream == 1) {
-      // Done, unless the workgroup takes part in an in-launch merge (below).
-      if (a.counters == nullptr || it.n_splits == 1) return;
-    } else {
-      const f32x4 h = x[ltid];
-      const float m1 = h[0], l1 = h[1];
-      const float mm = fmaxf(mref, m1);
-      const float base = mm == -INFINITY ? 0.f : mm;
-      const float w0 = fast_exp2(mref - base), w1 = fast_exp2(m1 - base);
-      sm.l = sm.l * w0 + l1 * w1;
-#pragma unroll
-      for (int d = 0; d < DT; ++d)
+      for (int dd = 0; dd < HB; ++dd)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f32x4 v = x[(1 + 4 * d + q) * LANES + ltid];
+          const int d = (1 - S) * HB + dd;
+          hand[(1 + 4 * dd + q) * LANES + ltid] =
+              f32x4{acc[d][4 * q], acc[d][4 * q + 1], acc[d][4 * q + 2], acc[d][4 * q + 3]};
+        }
+      __syncthreads();
+      const f32x4 h = got[ltid];
+      constexpr bool s0 = S == 0;
+      const float m0 = s0 ? mref : h[0], m1 = s0 ? h[0] : mref;
+      const float l0 = s0 ? sm.l : h[1], l1 = s0 ? h[1] : sm.l;
+      const float mm = fmaxf(m0, m1);
+      const float base = mm == -INFINITY ? 0.f : mm;
+      const float w0 = fast_exp2(m0 - base), w1 = fast_exp2(m1 - base);
+      // One explicit rounding order, so that both streams hold the same l.
+      sm.l = __builtin_fmaf(l0, w0, l1 * w1);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[d][4 * q + e] = acc[d][4 * q + e] * w0 + v[e] * w1;
+      for (int dd = 0; dd < HB; ++dd)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = S * HB + dd;
+          const f32x4 v = got[(1 + 4 * dd + q) * LANES + ltid];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float own = acc[d][4 * q + e];
+            const float a0 = s0 ? own : v[e], a1 = s0 ? v[e] : own;
+            acc[d][4 * q + e] = __builtin_fmaf(a0, w0, a1 * w1);
+          }
         }
       mref = mm;
-    }
-  }
-
-  const float l_tot = xor32_sum(sm.l);
-  // Result rows through the LDS, now free: the tile buffers of stream 1 (past
-  // the hand-over area) or, with one stream, the tile buffers, whose last
-  // reads and DMA pieces ended at the loop's last barrier.
-  const uint32_t area = lds_addr(smem) + (NS == 2 ? Lds<D>::bytes : 0);
-  if (a.counters == nullptr || it.n_splits == 1) {
+      const float l_tot = xor32_sum(sm.l);
+      // Result rows through stream 1's tile buffers, past the hand-over area.
+      const uint32_t area = lds_addr(smem) + Lds<D>::bytes;
+      float* const ax = reinterpret_cast<float*>(x + 2 * NV * LANES);
+      if (!merge_here) {
+        store_result_halves<D, T, S>(a, it, q0, wave * 32, g, lane, ltid, wave_active, acc,
+                                     l_tot, mref, area, ax);
+        return;
+      }
+      // Split, merged in this launch: store the partial, then every wave
+      // arrives (arrive_split_group); the last split of the group merges.
+      store_result_halves<D, T, S, kScDevice>(a, it, q0, wave * 32, g, lane, ltid, wave_active,
+                                              acc, l_tot, mref, area, ax);
+      static_assert((kBM * (kPMergeSplits + 1) + 1) * 4 <= Lds<D>::bytes,
+                    "merge scratch below the row area");
+      arrive_split_group<D, T, kBM, 64 * kNW * NS, 2>(a, it, q0, smem);
+    };
+    if (stream == 0) epilogue(std::integral_constant<int, 0>{});
+    else epilogue(std::integral_constant<int, 1>{});
+  } else {
+    const float l_tot = xor32_sum(sm.l);
+    // Result rows through the tile buffers, whose last reads and DMA pieces
+    // ended at the loop's last barrier. One stream never merges in the launch.
     if (!wave_active) return;
-    store_result_staged<D, T>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref, area);
-    return;
+    store_result_staged<D, T>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref,
+                              lds_addr(smem));
   }
-  // Split, merged in this launch: stream 0 stores the partial, then every
-  // wave arrives (arrive_split_group); the last split of the group merges.
-  if (wave_active && stream == 0)
-    store_result_staged<D, T, kScDevice>(a, it, kBM, q0, wave * 32, g, lane, acc, l_tot, mref,
-                                         area);
-  static_assert((kBM * (kPMergeSplits + 1) + 1) * 4 <= (NS == 2 ? Lds<D>::bytes : 0) ||
-                    NS == 1,
-                "merge scratch below the row area");
-  arrive_split_group<D, T, kBM, 64 * kNW * NS, 2>(a, it, q0, smem);
 }
 
 // ---------------------------------------------------------------------------
