@@ -194,9 +194,9 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  * arrival counters of the kernels that merge key splits in the same launch
  * (by default the prefill kernel and the decode kernel on ragged batches; the
  * one-launch decode kernel under DX_TUNE_ATTN_KERNEL 4): they must be zero
- * before a workspace is first used,
- * and every completed call leaves them zero. The rest needs no
- * initialisation. Calls that share a workspace must not overlap.
+ * before a workspace is first used, and every completed call leaves them
+ * zero. The rest needs no initialisation. Calls that share a workspace must
+ * not overlap.
  * Replaces: ops/gfx1151/attention/blockwise_causal.py:146-173.
  */
 int dx_blockwise_causal_attention(
