@@ -35,19 +35,20 @@
 // arithmetic.
 //
 // Pipeline. A stream is four waves (128 queries); waves whose 32 queries
-// are all past the end only help load. K/V tiles of 64 keys go global ->
-// registers -> LDS (double buffered, one barrier per tile), the next tile's
-// loads in flight behind the current tile's compute. Prefill runs one stream
-// per workgroup, two workgroups per CU. Decode-shaped calls (short query
-// chunk, long cache) run two streams per workgroup on alternate tiles of the
-// same key range -- two waves per SIMD, so one stream's softmax overlaps the
-// other's MFMAs -- and merge them through LDS, halving the split-KV partials
-// two separate workgroups would write.
+// are all past the end only help load. Decode-shaped calls (short query
+// chunk, long cache) run two streams per workgroup on alternate key tiles of
+// the same range (global -> registers -> LDS, double buffered, the next
+// tile's loads in flight behind the current tile's compute) -- two waves per
+// SIMD, so one stream's softmax overlaps the other's MFMAs -- and merge the
+// streams through LDS, halving the split-KV partials two separate workgroups
+// would write. Prefill runs two groups of four waves on 256 queries, half a
+// key tile apart, with K/V tiles moved to LDS by DMA (attn_pair_kernel).
 //
 // Work decomposition. A work item is (batch, head, query tile, key split).
 // Short query chunks over long caches split the key range over several
-// workgroups (split-KV) and a second kernel merges the partial
-// (max, sum, acc) triples. Items are issued heaviest-first, and when the
+// workgroups (split-KV) and the partial (max, sum, acc) triples are merged
+// either by a second kernel or, in the same launch, by the last split of the
+// group to finish (arrive_split_group). Items are issued heaviest-first, and when the
 // number of heads per segment is a multiple of 8 every item of one head lands
 // on one XCD (item i runs on XCD i % 8), so its K/V and partials stay in one
 // L2. Ragged batches (one cache length per sequence) get one segment per
