@@ -206,10 +206,10 @@ def run_headline(args, device):
     }
 
 
-def run_config(name: str, device, reps: int) -> dict:
-    """Attention alone at one config, per call: event-timed replays of a graph of n calls
-    on n distinct copies of the inputs (n chosen so that they exceed the 256 MB MALL, as
-    a model's per-layer caches do; the replay overhead is shared by the n calls)."""
+def _config_graph(name: str, device):
+    """A captured graph of n attention calls at one config on n distinct copies of the
+    inputs (n chosen so that they exceed the 256 MB MALL, as a model's per-layer caches
+    do). Returns (config, graph, n)."""
     import math
 
     import torch
@@ -260,8 +260,17 @@ def run_config(name: str, device, reps: int) -> dict:
     copies = [args] + [tuple(None if t is None else t.clone() for t in args)
                        for _ in range(n - 1)]
     graph = harness.capture(lambda: [one(*a) for a in copies])
+    return cfg, graph, n
+
+
+def run_config(name: str, device, reps: int) -> dict:
+    """Attention alone at one config, per call: event-timed replays of a graph of n calls
+    on n distinct copies of the inputs (the replay overhead is shared by the n calls)."""
+    from dexter_amd.bench import harness
+
+    cfg, graph, n = _config_graph(name, device)
     ms = harness.event_time_ms(graph.replay, reps=reps) / n
-    del graph, copies
+    del graph
     return {
         "us": ms * 1e3,
         "tflops": cfg.flops() / (ms * 1e-3) / 1e12,
@@ -272,6 +281,80 @@ def run_config(name: str, device, reps: int) -> dict:
         "bytes": cfg.bytes(),
         "calls_per_graph": n,
     }
+
+
+def run_timeline(name: str, device, reps: int) -> dict:
+    """Phase timeline of the decode kernel's last call in one replay of the config's graph
+    (`_config_graph`), from the timeline build's per-workgroup s_memrealtime stamps (100 MHz;
+    the words are listed at g_timeline in csrc/attn_fwd.hip). Medians per (sequence, split
+    count) over the workgroups, in us from the call's first workgroup start; the merge
+    kernel's blocks (if any) as one span. Stamps mark instructions issued: a store's
+    completion is not in them."""
+    import ctypes
+    import statistics
+
+    import torch
+
+    from dexter_amd.bench import harness
+    from dexter_amd.ops.gfx950 import _lib
+
+    lib = _lib.load()
+    if not hasattr(lib, "dx_timeline_read"):
+        raise RuntimeError(f"{_lib.LIB_PATH.name} has no stamps: build it with "
+                           "`python dexter-labs_amd/csrc/build.py --timeline`")
+    lib.dx_timeline_words.restype = ctypes.c_int64
+    cfg, graph, n = _config_graph(name, device)
+    per_call_us = harness.event_time_ms(graph.replay, reps=reps) / n * 1e3
+    words = lib.dx_timeline_words()
+    buf = (ctypes.c_uint64 * words)()
+    if lib.dx_timeline_clear() != 0:
+        raise RuntimeError("dx_timeline_clear failed")
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    if lib.dx_timeline_read(buf) != 0:
+        raise RuntimeError("dx_timeline_read failed")
+    slots, groups = 32, 2048
+    rows = [buf[w * slots:(w + 1) * slots] for w in range(groups)]
+    rows = [r for r in rows if r[0]]
+    merge = [(buf[slots * groups + 2 * i], buf[slots * groups + 2 * i + 1])
+             for i in range(8 * groups)]
+    merge = [m for m in merge if m[0]]
+    t0 = min(r[0] for r in rows)
+    us = lambda t: round((t - t0) / 100, 2)
+    med = lambda v: round(statistics.median(v), 2) if v else None
+    segs = {}
+    for r in rows:
+        segs.setdefault((r[8] >> 16 & 0xffff, r[8] >> 8 & 0xff), []).append(r)
+    out = {"config": name, "per_call_us": round(per_call_us, 2), "calls_per_graph": n,
+           "workgroups": len(rows), "span_us": us(max(r[7] for r in rows if r[7])),
+           "segments": []}
+    names = {1: "q_ready", 2: "loop_done", 3: "handover_done", 4: "stores_issued",
+             5: "arrived", 7: "end"}
+    for (b, ns), rs in sorted(segs.items()):
+        seg = {"batch": b, "splits": ns, "workgroups": len(rs),
+               "tiles": max(r[9] & 0xffff for r in rs), "rounds": max(r[9] >> 16 for r in rs),
+               "start": med([us(r[0]) for r in rs]), "start_max": max(us(r[0]) for r in rs)}
+        for k, label in names.items():
+            seg[label] = med([us(r[k]) for r in rs if r[k]])
+        seg["end_max"] = max((us(r[7]) for r in rs if r[7]), default=None)
+        seg["round_tiles_in_lds"] = [med([us(r[16 + i]) for r in rs if r[16 + i]])
+                                     for i in range(min(seg["rounds"], 16))]
+        mergers = [r for r in rs if r[8] >> 32]
+        if mergers:
+            seg["mergers"] = {"n": len(mergers),
+                              "arrived": med([us(r[5]) for r in mergers]),
+                              "merge_loads_done": med([us(r[6]) for r in mergers]),
+                              "end": med([us(r[7]) for r in mergers]),
+                              "end_max": max(us(r[7]) for r in mergers)}
+        out["segments"].append(seg)
+    if merge:
+        ends = [m[1] for m in merge if m[1]]
+        out["merge_kernel"] = {"blocks": len(merge), "first_start": us(min(m[0] for m in merge)),
+                               "median_start": med([us(m[0]) for m in merge]),
+                               "last_end": us(max(ends)) if ends else None}
+    del graph
+    return out
 
 
 def run_gemm_ceiling(device, reps: int = 10) -> dict:
@@ -494,6 +577,9 @@ def main() -> int:
     ap.add_argument("--only", choices=["C1", "C2", "C3", "C4", "norm", "cross", "qkv", "gemm"],
                     default=None,
                     help="time one config's attention only (for profiling runs)")
+    ap.add_argument("--timeline", choices=["C1", "C4"], default=None,
+                    help="phase timeline of one config's decode call (needs the library that "
+                         "`csrc/build.py --timeline` builds)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run a plain device copy of this size (counter calibration)")
     args = ap.parse_args()
@@ -514,6 +600,8 @@ def main() -> int:
     import dexter_amd.ops  # noqa: F401
     from dexter_amd.ops.gfx950 import _lib
 
+    if args.timeline:
+        _lib.LIB_PATH = _lib.LIB_PATH.with_name("libdexter_gfx950_timeline.so")
     _lib.load()  # fail loudly if the HIP library is missing
 
     if args.copy_mb:
@@ -525,6 +613,11 @@ def main() -> int:
         print(f"copy calibration: {n} bytes read, {n} bytes written", file=sys.stderr, flush=True)
         del src, dst
 
+    if args.timeline:
+        print(json.dumps({"timeline": args.timeline,
+                          **run_timeline(args.timeline, device, reps=max(10, args.steps))}),
+              flush=True)
+        return 0
     if args.only == "gemm":
         print(json.dumps({"only": "gemm", **run_gemm_ceiling(device, reps=max(10, args.steps))}),
               flush=True)

@@ -69,6 +69,38 @@
 namespace dx {
 namespace {
 
+// Phase stamps of the timeline build (`build.py --timeline`, which defines
+// DX_TIMELINE and writes a library of its own; the product library has no
+// stamps). Thread 0 of workgroup w < kTimelineGroups of the decode kernel
+// writes the device's 100 MHz s_memrealtime clock into word k of row w of
+// g_timeline (kTimelineSlots words a row); the merge kernel writes its
+// block's start and end into g_timeline_merge. Words:
+//   0 start, 1 Q in registers, 2 tile loop done, 3 stream hand-over done,
+//   4 result stores issued, 5 arrival counted (split merged in the launch),
+//   6 merge loads combined (the merging split), 7 end (stores issued);
+//   8 split | n_splits << 8 | batch << 16 | merge state << 32,
+//   9 tiles | barrier rounds << 16, 10 XCD; 16 + i: round i's tiles in LDS.
+#ifdef DX_TIMELINE
+constexpr int kTimelineSlots = 32, kTimelineGroups = 2048;
+__device__ uint64_t g_timeline[kTimelineSlots * kTimelineGroups];
+__device__ uint64_t g_timeline_merge[2 * 8 * kTimelineGroups];
+__device__ __forceinline__ void timeline_word(int k, uint64_t v) {
+  if (threadIdx.x == 0 && blockIdx.x < unsigned(kTimelineGroups))
+    g_timeline[blockIdx.x * kTimelineSlots + k] = v;
+}
+__device__ __forceinline__ void timeline_merge_word(int k) {
+  if (threadIdx.x == 0 && blockIdx.x < unsigned(8 * kTimelineGroups))
+    g_timeline_merge[2 * blockIdx.x + k] = __builtin_amdgcn_s_memrealtime();
+}
+#define DX_STAMP(k) timeline_word((k), __builtin_amdgcn_s_memrealtime())
+#define DX_NOTE(k, v) timeline_word((k), uint64_t(v))
+#define DX_MERGE_STAMP(k) timeline_merge_word(k)
+#else
+#define DX_STAMP(k) ((void)0)
+#define DX_NOTE(k, v) ((void)0)
+#define DX_MERGE_STAMP(k) ((void)0)
+#endif
+
 constexpr int kBN = 64;        // keys per tile
 constexpr int kNW = 4;         // waves per workgroup
 constexpr int kBM = 32 * kNW;  // queries per workgroup
@@ -1305,6 +1337,7 @@ __device__ __forceinline__ void merge_split_group(const AttnArgs& a, const Coord
       }
     }
   }
+  DX_STAMP(6);
 #pragma unroll
   for (int k = 0; k < UPT; ++k) {
     const int u = t + NT * k, r = u / CR, ch = u % CR;
@@ -1349,10 +1382,15 @@ __device__ __forceinline__ void arrive_split_group(const AttnArgs& a, const Coor
   }
   __syncthreads();
   const int state = *last;
+  DX_STAMP(5);
+  DX_NOTE(8, uint32_t(it.split) | uint32_t(it.n_splits) << 8 | uint32_t(it.b) << 16 |
+                 uint64_t(state) << 32);
+  DX_STAMP(7);  // the merging split writes it again when done
   if (state == 0) return;
   const int nrows = min(BM, a.Lq - q0);
   if (state == 1) merge_split_group<D, T, BM, NT, SB, kScXcd>(a, it, q0, nrows, smem);
   else merge_split_group<D, T, BM, NT, SB, kScDevice>(a, it, q0, nrows, smem);
+  DX_STAMP(7);
 }
 
 // The dual-stream kernel's results after its split hand-over: stream s holds
@@ -1450,6 +1488,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   prefetch_args(a);
 
   const Coord it = locate(a, blockIdx.x, false, 0);
+  DX_STAMP(0);
   const int b = it.b, h = it.h;
   // NS streams of four waves; stream s takes every NS-th tile of the range.
   // Wave and stream indices are read through readfirstlane so the compiler
@@ -1571,6 +1610,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       for (int s = 0; s < KQ; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qx + 16 * s);
     }
     __syncthreads();  // exchange read before stream 1's first tile overwrites it
+    DX_STAMP(1);
   }
   {
     const uint32_t qmask = qvalid ? ~0u : 0u;
@@ -1634,6 +1674,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     uint16_t* const st = region + (i & 1) * Lds<D>::stage;
     if (t < t_end) regs.store(ltid, st, st + Lds<D>::kElems);
     __syncthreads();
+    if (i < 16) DX_STAMP(16 + i);
     if (t + NS < t_end) regs.load(ltid, src, t + NS, true);
     const bool in_cache = t < n_ct;
     const int j0 = in_cache ? t * kBN : cache_len + (t - n_ct) * kBN;
@@ -1667,6 +1708,15 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       f32x4* const hand = x + S * NV * LANES;
       const f32x4* const got = x + (1 - S) * NV * LANES;
       __syncthreads();  // all tile reads done: the LDS is free
+      DX_STAMP(2);
+      DX_NOTE(9, uint32_t(t_end - t_begin) | uint32_t(iters) << 16);
+#ifdef DX_TIMELINE
+      {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+        DX_NOTE(10, xcc);
+      }
+#endif
       hand[ltid] = f32x4{mref, sm.l, 0.f, 0.f};
 #pragma unroll
       for (int dd = 0; dd < HB; ++dd)
@@ -1677,6 +1727,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
               f32x4{acc[d][4 * q], acc[d][4 * q + 1], acc[d][4 * q + 2], acc[d][4 * q + 3]};
         }
       __syncthreads();
+      DX_STAMP(3);
       const f32x4 h = got[ltid];
       constexpr bool s0 = S == 0;
       const float m0 = s0 ? mref : h[0], m1 = s0 ? h[0] : mref;
@@ -1707,12 +1758,16 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       if (!merge_here) {
         store_result_halves<D, T, S>(a, it, q0, wave * 32, g, lane, ltid, wave_active, acc,
                                      l_tot, mref, area, ax);
+        DX_STAMP(4);
+        DX_NOTE(8, uint32_t(it.split) | uint32_t(it.n_splits) << 8 | uint32_t(it.b) << 16);
+        DX_STAMP(7);
         return;
       }
       // Split, merged in this launch: store the partial, then every wave
       // arrives (arrive_split_group); the last split of the group merges.
       store_result_halves<D, T, S, kScDevice>(a, it, q0, wave * 32, g, lane, ltid, wave_active,
                                               acc, l_tot, mref, area, ax);
+      DX_STAMP(4);
       static_assert((kBM * (kPMergeSplits + 1) + 1) * 4 <= Lds<D>::bytes,
                     "merge scratch below the row area");
       arrive_split_group<D, T, kBM, 64 * kNW * NS, 2>(a, it, q0, smem);
@@ -2857,6 +2912,7 @@ template <int D> struct CombineShape {
 // one (batch, head) run on the XCD whose L2 holds that head's partials.
 template <int D, typename T, int NMAX>
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a) {
+  DX_MERGE_STAMP(0);
   prefetch_args(a);
   using CS = CombineShape<D>;
   // Blocks per work-item group: ceil(min(bm, Lq) / RPB), as the host sizes
@@ -2887,6 +2943,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs 
   w2[0] = Mfma<T>::pack(acc[0], acc[1]);
   w2[1] = Mfma<T>::pack(acc[2], acc[3]);
   __builtin_nontemporal_store(w2, reinterpret_cast<u32x2*>(op));
+  DX_MERGE_STAMP(1);
 }
 
 // ---------------------------------------------------------------------------
@@ -2934,6 +2991,7 @@ int64_t combine_bpt(int64_t D, int64_t bm) {
 }
 
 int bm_of(int kernel) { return kernel == kPaired ? kBMPair : kBM; }
+
 
 // Query-group rows and per-segment key splits of the one-launch decode
 // kernel, for segments of `units` (batch, head) pairs over tiles[i] key tiles
@@ -3528,3 +3586,28 @@ extern "C" int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t L
   if (B * Lq == 0) return 0;
   return make_plan(B, Lq, Lk, H, D, cache_len, cache_lens).ws_bytes;
 }
+
+#ifdef DX_TIMELINE
+// The timeline build's stamps (the words are described at g_timeline):
+// decode rows first, then the merge kernel's (start, end) pairs. Synchronous.
+extern "C" int64_t dx_timeline_words() {
+  return int64_t(sizeof(dx::g_timeline) + sizeof(dx::g_timeline_merge)) / 8;
+}
+extern "C" int dx_timeline_read(uint64_t* host) {
+  hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(dx::g_timeline), sizeof(dx::g_timeline),
+                                     0, hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    e = hipMemcpyFromSymbol(host + sizeof(dx::g_timeline) / 8, HIP_SYMBOL(dx::g_timeline_merge),
+                            sizeof(dx::g_timeline_merge), 0, hipMemcpyDeviceToHost);
+  return int(e);
+}
+extern "C" int dx_timeline_clear() {
+  static const uint64_t zeros[sizeof(dx::g_timeline) / 8] = {};
+  hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(dx::g_timeline), zeros, sizeof(dx::g_timeline), 0,
+                                   hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpyToSymbol(HIP_SYMBOL(dx::g_timeline_merge), zeros, sizeof(dx::g_timeline_merge),
+                          0, hipMemcpyHostToDevice);
+  return int(e);
+}
+#endif
