@@ -51,6 +51,15 @@ def test_library_resolves_all_of_its_own_symbols(built_lib):
     assert not own, f"undefined: {own}"
 
 
+def test_product_library_carries_no_phase_stamps(built_lib):
+    """The timeline build's readers (and so its stamp code) exist only in the measurement
+    library that `build.py --timeline` writes beside this one."""
+    lib = ctypes.CDLL(str(built_lib))
+    stamped = [n for n in ("dx_timeline_words", "dx_timeline_read", "dx_timeline_clear")
+               if hasattr(lib, n)]
+    assert not stamped, f"product library exports {stamped}"
+
+
 def test_loader_binds_exactly_the_header(built_lib):
     assert sorted(_lib.exported_symbols()) == declared_functions()
 
