@@ -314,7 +314,9 @@ def run_timeline(name: str, device, reps: int) -> dict:
     torch.cuda.synchronize()
     if lib.dx_timeline_read(buf) != 0:
         raise RuntimeError("dx_timeline_read failed")
-    slots, groups = 32, 2048
+    slots, groups = 32, 2048  # kTimelineSlots, kTimelineGroups (csrc/attn_fwd.hip)
+    if words != slots * groups + 2 * 8 * groups:
+        raise RuntimeError(f"timeline library layout changed: {words} words")
     rows = [buf[w * slots:(w + 1) * slots] for w in range(groups)]
     rows = [r for r in rows if r[0]]
     merge = [(buf[slots * groups + 2 * i], buf[slots * groups + 2 * i + 1])
