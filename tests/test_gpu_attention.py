@@ -284,6 +284,35 @@ def test_varlen_matches_per_sequence_calls(device, built_lib):
         assert_parity(one, ref)
 
 
+@pytest.mark.parametrize("q_len,cache_len,h", [(1, 65535, 8), (16, 32749, 8), (83, 16381, 24)])
+def test_long_cache_decode(device, built_lib, q_len, cache_len, h):
+    """Decode-shaped calls far past the benchmark's cache: up to 1,024 key tiles at the
+    planner's largest split count (16), cache lengths that leave a partial last tile, and
+    tile counts that do not divide evenly over the splits."""
+    b, d = 1, 128
+    q, k, v = (_rand((b, q_len, h, d), device, seed=60 + i) for i in range(3))
+    cache = _rand((2, b, cache_len + q_len, h, d), device, seed=63)
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len)
+    assert torch.isfinite(got).all()
+    assert_parity(got, _oracle(q, k, v, cache, cache_len, None), what=f"{q_len} x {cache_len}")
+
+
+def test_long_ragged_batch(device, built_lib):
+    """A ragged batch with one sequence of 40,000 cached keys and one with none: the long
+    sequence takes more splits than a merge inside the launch holds (the merge kernel runs)."""
+    h, d, q_len = 8, 128, 99
+    lens = [40000, 0]
+    b = len(lens)
+    q, k, v = (_rand((b, q_len, h, d), device, seed=70 + i) for i in range(3))
+    cache = _rand((2, b, max(lens), h, d), device, seed=73)
+    bb = torch.tensor([0, 83], device=device)
+    got = ops.blockwise_causal_attention_varlen(q, k, v, kv_cache=cache, cache_lens=lens,
+                                                block_boundaries=bb)
+    for i, c in enumerate(lens):
+        ref = _oracle(q[i:i + 1], k[i:i + 1], v[i:i + 1], cache[:, i:i + 1], c, bb)
+        assert_parity(got[i:i + 1], ref, what=f"seq {i} cache {c}")
+
+
 def test_kv_length_mismatch_with_a_mask_is_an_error(device, built_lib):
     """Lk != Lq is cross-attention (every key visible); with a causal or block
     mask it has no meaning (the mask is [q_len, cache_len + q_len]) and raises."""
