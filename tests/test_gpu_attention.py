@@ -284,14 +284,17 @@ def test_varlen_matches_per_sequence_calls(device, built_lib):
         assert_parity(one, ref)
 
 
-@pytest.mark.parametrize("q_len,cache_len,h", [(1, 65535, 8), (16, 32749, 8), (83, 16381, 24)])
-def test_long_cache_decode(device, built_lib, q_len, cache_len, h):
+@pytest.mark.parametrize("q_len,cache_len,h,d,dtype", [
+    (1, 65535, 8, 128, torch.bfloat16), (16, 32749, 8, 128, torch.bfloat16),
+    (83, 16381, 24, 128, torch.bfloat16), (1, 65535, 8, 64, torch.bfloat16),
+    (83, 16381, 24, 128, torch.float16)])
+def test_long_cache_decode(device, built_lib, q_len, cache_len, h, d, dtype):
     """Decode-shaped calls far past the benchmark's cache: up to 1,024 key tiles at the
     planner's largest split count (16), cache lengths that leave a partial last tile, and
-    tile counts that do not divide evenly over the splits."""
-    b, d = 1, 128
-    q, k, v = (_rand((b, q_len, h, d), device, seed=60 + i) for i in range(3))
-    cache = _rand((2, b, cache_len + q_len, h, d), device, seed=63)
+    tile counts that do not divide evenly over the splits; head_dim 64 and f16 too."""
+    b = 1
+    q, k, v = (_rand((b, q_len, h, d), device, dtype, seed=60 + i) for i in range(3))
+    cache = _rand((2, b, cache_len + q_len, h, d), device, dtype, seed=63)
     got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len)
     assert torch.isfinite(got).all()
     assert_parity(got, _oracle(q, k, v, cache, cache_len, None), what=f"{q_len} x {cache_len}")
