@@ -300,6 +300,22 @@ def test_long_cache_decode(device, built_lib, q_len, cache_len, h, d, dtype):
     assert_parity(got, _oracle(q, k, v, cache, cache_len, None), what=f"{q_len} x {cache_len}")
 
 
+@pytest.mark.parametrize("q_len,cache_len,h,blocks", [(1024, 15360, 4, None),
+                                                       (777, 20001, 8, [0, 333])])
+def test_long_chunked_prefill(device, built_lib, q_len, cache_len, h, blocks):
+    """Prefill-shaped chunks over long caches (the paired kernel, its key splits merged in
+    the launch), past the 8,217 keys of the largest benchmark chunk, with and without a block
+    list inside the chunk."""
+    b, d = 1, 128
+    q, k, v = (_rand((b, q_len, h, d), device, seed=80 + i) for i in range(3))
+    cache = _rand((2, b, cache_len + q_len, h, d), device, seed=83)
+    bb = torch.tensor(blocks, device=device) if blocks else None
+    got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
+                                         block_boundaries=bb)
+    assert_parity(got, _oracle(q, k, v, cache, cache_len, bb),
+                  what=f"{q_len} x {cache_len} blocks={blocks}")
+
+
 def test_long_ragged_batch(device, built_lib):
     """A ragged batch with one sequence of 40,000 cached keys and one with none: the long
     sequence takes more splits than a merge inside the launch holds (the merge kernel runs)."""
