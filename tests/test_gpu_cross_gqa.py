@@ -122,7 +122,8 @@ def test_groot_gqa_causal(device, built_lib, hkv):
     assert torch.equal(got, full), "grouped K/V differ from the materialised expansion"
 
 
-@pytest.mark.parametrize("case", ["decode_cache", "blocks", "prefill", "cross"])
+@pytest.mark.parametrize("case", ["decode_cache", "blocks", "prefill", "cross", "decode_long",
+                                  "chunk_long"])
 def test_gqa_paths_equal_the_expansion(device, built_lib, case):
     """Every kernel path with grouped K/V against the same path on expanded K/V
     (bit-exact) and the oracle (parity)."""
@@ -132,6 +133,12 @@ def test_gqa_paths_equal_the_expansion(device, built_lib, case):
     if case == "decode_cache":
         lq, cache_len = 83, 1245
         cache = _rand((2, 1, 1328, hkv, d), device, scale=0.5, seed=31)
+    elif case == "decode_long":  # one query over 32,749 cached keys: 16 splits
+        lq, cache_len = 1, 32749
+        cache = _rand((2, 1, cache_len + lq, hkv, d), device, scale=0.5, seed=35)
+    elif case == "chunk_long":  # a 512-query chunk over 12,001 cached keys
+        lq, cache_len = 512, 12001
+        cache = _rand((2, 1, cache_len + lq, hkv, d), device, scale=0.5, seed=36)
     elif case == "blocks":
         lq = 512
         bb = torch.tensor([0, 128, 256, 384], device=device)
