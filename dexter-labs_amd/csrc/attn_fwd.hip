@@ -237,17 +237,28 @@ __device__ __forceinline__ void for_each_block(const AttnArgs& a, Fn&& fn) {
   }
 }
 
+// Current keys [0, e) that the pair's column slice [cache_len : cache_len + hi]
+// of the reference's [Lq, cache_len + Lq] mask sets, by Python's slice rules:
+// min(hi, Lq) for hi >= 0; for a negative hi, nothing while the stop
+// cache_len + hi is still >= 0 (it lies before the slice's start), and once it
+// is negative it counts from the end of the key axis, leaving the current keys
+// [0, cache_len + Lq + hi) (at least none).
+__device__ __forceinline__ int pair_end(int hi, int cache_len, int Lq) {
+  if (hi >= 0) return min(hi, Lq);
+  return cache_len + hi < 0 ? max(cache_len + Lq + hi, 0) : 0;
+}
+
 // End (exclusive, in current-key coordinates) of the keys query i may see:
 // the union of the block pairs whose row slice holds i, i.e. the largest
-// min(hi, Lq) among them (a negative hi adds nothing), 0 when no pair holds
-// i (such a row sees only the cache). For ascending starts this is the end of
-// i's own block, and rows before the first start see no current key.
-__device__ __forceinline__ int visible_end(const AttnArgs& a, int i) {
+// pair_end among them, 0 when no pair holds i (such a row sees only the
+// cache). For ascending starts this is the end of i's own block, and rows
+// before the first start see no current key.
+__device__ __forceinline__ int visible_end(const AttnArgs& a, int i, int cache_len) {
   if (a.causal) return i + 1;
   if (a.n_blocks == 0) return a.Lk;
   int e = 0;
   for_each_block(a, [&](int lo, int hi) __attribute__((always_inline)) {
-    if (i >= slice_at(lo, a.Lq) && i < slice_at(hi, a.Lq)) e = max(e, min(hi, a.Lq));
+    if (i >= slice_at(lo, a.Lq) && i < slice_at(hi, a.Lq)) e = max(e, pair_end(hi, cache_len, a.Lq));
   });
   return e;
 }
@@ -262,8 +273,8 @@ __device__ __forceinline__ int visible_end(const AttnArgs& a, int i) {
 struct EndBounds { int lo, hi; };
 __device__ __forceinline__ EndBounds end_bounds(const AttnArgs& a, int q_first, int q_last) {
   if (a.causal || a.n_blocks == 0)
-    return {__builtin_amdgcn_readfirstlane(visible_end(a, q_first)),
-            __builtin_amdgcn_readfirstlane(visible_end(a, q_last))};
+    return {__builtin_amdgcn_readfirstlane(visible_end(a, q_first, 0)),
+            __builtin_amdgcn_readfirstlane(visible_end(a, q_last, 0))};
   bool ascending = true;
   int prev = 0;
   int e_first = 0, e_last = 0;
@@ -1588,7 +1599,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
   }
 
   // Visible-key end of this lane's query (per-key masking of straddling tiles).
-  const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
+  const int my_end = qvalid ? cache_len + visible_end(a, qi, cache_len) : 0;
 
   if (NS == 2) {
     // Exchange area: the first tile buffer of stream 1 (not yet written).
@@ -2033,7 +2044,7 @@ __global__ __launch_bounds__(64 * kPairWaves, 1) void attn_pair_kernel(AttnArgs 
   dma.init(wid, lane, src);
 #pragma unroll
   for (int m = 0; m < Dma::NP; ++m) dma.issue(m, src, smem_b, t_begin, nt, 0, -1, 0, 2, wid);
-  const int my_end = qvalid ? cache_len + visible_end(a, qi) : 0;
+  const int my_end = qvalid ? cache_len + visible_end(a, qi, cache_len) : 0;
   PairAddr<D> ad;
   ad.init(smem_b, lane);
 
@@ -2533,7 +2544,7 @@ __global__ __launch_bounds__(64 * (2 * NQW + 1), 1) void attn_decode_kernel(Attn
   } else {
     if (threadIdx.x < 16) sync[threadIdx.x] = 0;
     // Visible-key end of this lane's query (both key halves mask with it).
-    const int my_end = wave_active && qi < q_end ? cache_len + visible_end(a, min(qi, a.Lq - 1)) : 0;
+    const int my_end = wave_active && qi < q_end ? cache_len + visible_end(a, min(qi, a.Lq - 1), cache_len) : 0;
     PairAddr<D, kDecSlots> ad;
     ad.init(smem_b, lane);
     int na = 0;

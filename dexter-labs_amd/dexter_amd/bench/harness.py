@@ -17,7 +17,10 @@ import torch
 
 
 def capture(fn: Callable[[], object], warmup: int = 2) -> torch.cuda.CUDAGraph:
-    """Run ``fn`` eagerly ``warmup`` times on a side stream, then capture it once."""
+    """Run ``fn`` eagerly ``warmup`` times on a side stream, then capture it once
+    on that same stream, so per-stream state the calls set up while warming up
+    (the attention workspace) is what the graph records, not a new allocation
+    and its zero fill inside the graph."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -26,7 +29,7 @@ def capture(fn: Callable[[], object], warmup: int = 2) -> torch.cuda.CUDAGraph:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         fn()
     torch.cuda.synchronize()
     return graph

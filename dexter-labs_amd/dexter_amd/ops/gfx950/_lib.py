@@ -209,28 +209,45 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_tuning_values: dict[int, int] = {}
+
+
 def set_tuning(key: int, value: int) -> None:
     """Process-wide launch-schedule override (0 restores the library's choice)."""
     check(load().dx_set_tuning(int(key), int(value)), "set_tuning")
+    _tuning_values[int(key)] = int(value)
+
+
+def get_tuning(key: int) -> int:
+    """The override last set through ``set_tuning`` for ``key`` (0: none)."""
+    return _tuning_values.get(int(key), 0)
 
 
 class tuning:
     """Context manager for launch-schedule overrides, e.g.
-    ``with tuning(TUNE_ATTN_SPLITS, 4): ...``; restores automatic choice on exit."""
+    ``with tuning(TUNE_ATTN_SPLITS, 4): ...``; on exit the key gets back the
+    value it had on entry, so nested contexts and an outer ``set_tuning``
+    survive an inner context."""
 
     def __init__(self, key: int, value: int) -> None:
         self.key, self.value = key, value
+        self.saved = 0
 
     def __enter__(self) -> "tuning":
+        self.saved = get_tuning(self.key)
         set_tuning(self.key, self.value)
         return self
 
     def __exit__(self, *exc) -> None:
-        set_tuning(self.key, 0)
+        set_tuning(self.key, self.saved)
 
 
 _ws_lock = threading.Lock()
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Outgrown workspaces, never released: a graph captured while one was current
+# replays with its address, so its memory must not go back to the allocator.
+# Growth doubles, so these hold less than the current buffers do.
+_retired: list[torch.Tensor] = []
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -239,8 +256,11 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     One buffer per (device, stream), kept between calls and grown when needed.
     The attention kernels keep arrival counters in it that must be zero when a
     call starts and that every call leaves at zero, so the buffer is zeroed
-    once, when it is allocated (a fill kernel, which graph capture records).
-    Calls on one stream are ordered, so they never share it concurrently.
+    once, when it is allocated. Calls on one stream are ordered, so they never
+    share it concurrently. A buffer first needed under graph capture is
+    allocated in the graph's memory pool and its zero fill is recorded (each
+    replay clears it again, which is harmless): warm a captured call up on the
+    capture stream (``runtime.capture`` and the bench do) to keep the fill out.
     """
     if nbytes <= 0:
         return None
@@ -250,6 +270,8 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
             size = max(nbytes, 2 * buf.numel() if buf is not None else 0)
+            if buf is not None:
+                _retired.append(buf)
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
             _workspaces[key] = buf
     return buf

@@ -11,8 +11,8 @@ What differs is the table of known parts. The reference knows RDNA3/3.5
 (``platform.py:201-208``); this module knows CDNA4 (gfx950, MI355X): wave64,
 MFMA matrix cores with bf16/f16/fp8/int8 inputs, 160 KB of LDS per CU, HBM3E,
 and ``global_load_lds`` (direct global→LDS copies). An unknown AMD part still
-raises, with the same wording, because a kernel picked on a guessed platform
-is worse than no kernel.
+raises ``RuntimeError`` (naming the part and the architectures this table
+knows), because a kernel picked on a guessed platform is worse than no kernel.
 """
 
 from __future__ import annotations

@@ -73,7 +73,10 @@ def _as_tuple(out) -> tuple[torch.Tensor, ...]:
 def _record(fn: Callable[..., object], static: tuple[torch.Tensor, ...], warmup: int,
             after_each_warmup: Callable[[], None] | None = None) -> GraphRunner:
     """Run ``fn(*static)`` ``warmup`` times on a side stream (so module loads and
-    allocator growth happen outside the recording), then record one call.
+    allocator growth happen outside the recording), then record one call on
+    that same stream (per-stream state set up while warming up, such as the
+    attention workspace, is then reused rather than allocated and zero-filled
+    inside the graph).
 
     ``after_each_warmup`` runs after every eager call, still on the side stream.
     """
@@ -87,7 +90,7 @@ def _record(fn: Callable[..., object], static: tuple[torch.Tensor, ...], warmup:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         outputs = _as_tuple(fn(*static))
     return GraphRunner(graph, static, outputs)
 

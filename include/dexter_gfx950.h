@@ -171,8 +171,14 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  *   query i sees key j iff j < cache_len + end(i), where end(i) is
  *     causal != 0          : i + 1
  *     n_blocks == 0        : Lk (one block: every current key)
- *     otherwise            : the largest block end among blocks [s_b, s_{b+1})
- *                            (last end = Lq) containing i; 0 if none does
+ *     otherwise            : the union over the pairs (lo, hi) of consecutive
+ *                            entries of (starts..., Lq) whose row slice
+ *                            [lo:hi] holds i (Python slicing over Lq rows),
+ *                            of pair_end(hi): min(hi, Lq) for hi >= 0; for
+ *                            hi < 0, max(cache_len + Lq + hi, 0) when
+ *                            cache_len + hi < 0 (the reference's column stop
+ *                            cache_len + hi then counts from the end of the
+ *                            key axis), else 0; 0 if no pair holds i
  *   (ops/reference/attention.py:22-47). With causal or block starts Lk must
  *   equal Lq, as the reference's mask shape requires. Lk != Lq with
  *   n_blocks == 0 and causal == 0 is cross-attention: every key visible (the
@@ -183,8 +189,10 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  *   multiple of Hkv; query head h reads K/V head h / (H / Hkv), the head that
  *   k.repeat_interleave(H / Hkv, dim=2) would put at h (vla/groot/backbone.py:109-114).
  * block_starts: device pointer to n_blocks int32 (starts_dtype DX_I32) or
- * int64 (DX_I64) block start indices, read on the device (no host sync),
- * sorted ascending (the reference builds them with torch.arange).
+ * int64 (DX_I64) block start indices, read on the device (no host sync), in
+ * any order and of any sign, as the reference takes them; ascending
+ * non-negative starts (the reference builds them with torch.arange) let the
+ * kernels skip whole future tiles, any other list is masked key by key.
  * softmax_scale multiplies q.k before the softmax (the reference's default
  * is 1/sqrt(D); callers pass it explicitly). dtype: DX_BF16 or DX_F16;
  * D: 64 or 128.

@@ -5,8 +5,11 @@ Follows ``python/dexter/ops/reference/attention.py``:
 * mask (:22-47): ``[q_len, cache_len + q_len]``; the cached history is always
   visible (:31); ``causal`` is token-causal on the current keys (:33-37);
   ``block_boundaries is None`` makes every current key visible (:39-41);
-  otherwise block ``[lo, hi)`` (starts plus a final ``q_len``) sees current
-  keys ``[0, hi)`` (:43-46).
+  otherwise each pair ``(lo, hi)`` of consecutive entries of the starts plus a
+  final ``q_len`` sets ``mask[lo:hi, cache_len : cache_len + hi]`` (:43-46),
+  Python's slice rules included: rows ``[lo:hi]`` of ``q_len``, and current
+  keys ``[0, pair_end(hi))``, where a stop ``cache_len + hi`` below zero
+  counts from the end of the whole key axis.
 * op (:50-77): default scale ``1/sqrt(D)`` (:63); cache rows ``[:cache_len]``
   in front of k/v (:65-67); fp32 logits (:71); ``-inf`` fill (:74); softmax
   then ``@ v`` in fp32 (:76); cast to q's dtype (:77).
@@ -52,8 +55,24 @@ def visible_end(q_len: int, cache_len: int, block_boundaries, causal: bool = Fal
     for lo, hi in zip(bounds[:-1], bounds[1:]):
         # Python slicing, as the reference's mask[lo:hi, ...] uses.
         seg = end[lo:hi]
-        end[lo:hi] = torch.clamp(seg, min=min(hi, q_len))
+        end[lo:hi] = torch.clamp(seg, min=pair_end(hi, cache_len, q_len))
     return cache_len + end
+
+
+def pair_end(hi: int, cache_len: int, q_len: int) -> int:
+    """Current keys ``[0, e)`` that the reference's column slice
+    ``mask[..., cache_len : cache_len + hi]`` sets on a ``cache_len + q_len``
+    key axis (``ops/reference/attention.py:45``), by Python's slice rules.
+
+    ``hi >= 0``: the stop clamps at the axis end, ``e = min(hi, q_len)``.
+    ``-cache_len <= hi < 0``: the stop lies before the start, nothing.
+    ``hi < -cache_len``: the negative stop counts from the axis end,
+    ``cache_len + q_len + hi`` in absolute columns, so the current keys up to
+    ``cache_len + q_len + hi`` (at least 0) are set.
+    """
+    if hi >= 0:
+        return min(hi, q_len)
+    return max(cache_len + q_len + hi, 0) if cache_len + hi < 0 else 0
 
 
 def block_causal_mask(q_len: int, cache_len: int, block_boundaries, device=None,

@@ -19,7 +19,13 @@ import numpy as np
 
 
 def key_visible(i: int, j: int, q_len: int, cache_len: int, starts, causal: bool) -> bool:
-    """Whether query ``i`` may attend to key ``j`` (key 0 = first cached row)."""
+    """Whether query ``i`` may attend to key ``j`` (key 0 = first cached row).
+
+    Block pairs follow the reference's ``mask[lo:hi, cache_len:cache_len + hi]``
+    (``ops/reference/attention.py:43-46``) through membership in sliced
+    ``range`` objects, which apply Python's slice rules (negative bounds count
+    from the end, out-of-range bounds clamp) without restating them.
+    """
     if j < cache_len:
         return True
     jj = j - cache_len
@@ -28,10 +34,36 @@ def key_visible(i: int, j: int, q_len: int, cache_len: int, starts, causal: bool
     if starts is None:
         return True
     bounds = list(starts) + [q_len]
+    rows, cols = range(q_len), range(cache_len + q_len)
     for lo, hi in zip(bounds[:-1], bounds[1:]):
-        if lo <= i < hi and jj < hi:
+        if i in rows[lo:hi] and j in cols[cache_len:cache_len + hi]:
             return True
     return False
+
+
+def slice_mask(q_len: int, cache_len: int, starts, causal: bool = False):
+    """The reference's mask as nested Python lists of bools, built with real
+    slice assignment on each row list, step by step as
+    ``ops/reference/attention.py:30-46`` builds its tensor."""
+    n = cache_len + q_len
+    mask = [[False] * n for _ in range(q_len)]
+    for row in mask:
+        row[:cache_len] = [True] * len(row[:cache_len])
+    if causal:
+        for r, row in enumerate(mask):
+            for c in range(q_len):
+                row[cache_len + c] = c <= r
+        return mask
+    if starts is None:
+        for row in mask:
+            row[cache_len:] = [True] * len(row[cache_len:])
+        return mask
+    bounds = list(starts) + [q_len]
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        for row in mask[lo:hi]:
+            seg = row[cache_len:cache_len + hi]
+            row[cache_len:cache_len + hi] = [True] * len(seg)
+    return mask
 
 
 def attention(q, k, v, cache_k=None, cache_v=None, cache_len=0, starts=None,

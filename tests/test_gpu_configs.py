@@ -30,7 +30,15 @@ pytestmark = pytest.mark.gpu
 
 
 def _oracle_attention_chunked(q, k, v, cache, cache_len, bb, heads_per_chunk=4):
-    """fp32 oracle on q's device, a few heads at a time (bounded memory)."""
+    """fp32 oracle on q's device, a few heads at a time (bounded memory).
+
+    On the GPU the oracle's products are torch's fp32 GEMMs, which must stay
+    full fp32: TF32 (xf32 on ROCm) would round their operands to 10-bit
+    mantissas, a coarser reference than the bf16 kernel it checks.
+    """
+    if q.is_cuda:
+        assert not torch.backends.cuda.matmul.allow_tf32, "oracle GEMMs must be full fp32"
+        assert torch.get_float32_matmul_precision() == "highest", "oracle GEMMs must be full fp32"
     outs = []
     for h0 in range(0, q.shape[2], heads_per_chunk):
         hs = slice(h0, h0 + heads_per_chunk)

@@ -152,6 +152,36 @@ def test_unordered_block_lists_match_reference(device, built_lib, path, blocks):
     assert_parity(got, _oracle(q, k, v, cache, c, bb), what=f"{name} blocks {blocks}")
 
 
+SHORT_CACHE_LISTS = [[0, -40, 83], [0, -82, 83], [0, -60, 30, -70], [50, 20], [-90, 10]]
+
+
+@pytest.mark.parametrize("path", PATHS, ids=[p[0] for p in PATHS])
+@pytest.mark.parametrize("cache_len", [0, 10, 39])
+@pytest.mark.parametrize("blocks", SHORT_CACHE_LISTS, ids=[str(b) for b in SHORT_CACHE_LISTS])
+def test_negative_starts_on_short_caches(device, built_lib, path, cache_len, blocks):
+    """Negative starts whose column stop ``cache_len + hi`` falls below zero:
+    the reference's slice then counts from the end of the key axis
+    (``ops/reference/attention.py:45``), so those rows see current keys
+    ``[0, cache_len + 83 + hi)``. Rows that see no key are NaN in both (the
+    reference's softmax over an all ``-inf`` row); the rest meet the bar."""
+    name, kernel, merge = path
+    b, l, h, d = 1, 83, 8, 128
+    q, k, v = (_rand((b, l, h, d), device, seed=340 + i) for i in range(3))
+    cache = _rand((2, b, cache_len + l, h, d), device, seed=343) if cache_len else None
+    bb = torch.tensor(blocks, dtype=torch.int64, device=device)
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, kernel), _lib.tuning(_lib.TUNE_ATTN_MERGE, merge):
+        got = ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=cache_len,
+                                             block_boundaries=bb)
+    torch.cuda.synchronize()
+    ref = _oracle(q, k, v, cache, cache_len, bb)
+    g = got.float().cpu()
+    nan_ref = torch.isnan(ref)
+    assert torch.equal(torch.isnan(g), nan_ref), f"{name} {blocks} cache {cache_len}: NaN rows differ"
+    keep = ~nan_ref.all(dim=-1).all(dim=-1).squeeze(0)
+    assert keep.any()
+    assert_parity(got[:, keep], ref[:, keep], what=f"{name} blocks {blocks} cache {cache_len}")
+
+
 @pytest.mark.parametrize("path", PATHS, ids=[p[0] for p in PATHS])
 @pytest.mark.parametrize("q_len,k_len,cache_len", [(1, 1, 0), (1, 100, 0), (1, 83, 300),
                                                    (2, 1, 0), (33, 70, 0)])

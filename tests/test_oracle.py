@@ -55,6 +55,72 @@ def test_mask_matches_brute_rule(cache_len, mode):
             assert bool(mask[i, j]) == brute.key_visible(i, j, q_len, cache_len, starts, causal)
 
 
+# Block lists the reference accepts beyond ascending starts: unsorted,
+# overlapping and negative entries (the GPU tests run the same lists).
+ODD_BLOCK_LISTS = [[0, 50, 30], [40, 0, 83], [30, 0, 60, 10], [0, -40, 83], [50, 20],
+                   [0, 83, 20, 60], [-90, 10], [0, -100, 40], [-5, -83, 2], [0, -82, 83],
+                   [0, -60, 30, -70]]
+
+
+@pytest.mark.parametrize("cache_len", [0, 10, 39, 300])
+@pytest.mark.parametrize("starts", ODD_BLOCK_LISTS, ids=[str(s) for s in ODD_BLOCK_LISTS])
+def test_mask_matches_python_slices_on_odd_lists(cache_len, starts):
+    """The oracle's mask equals the reference's construction done with real
+    slice assignment on nested lists (``brute.slice_mask``) and the per-key
+    rule of ``brute.key_visible``, for lists in any order and negative starts,
+    including stops ``cache_len + hi`` below zero, which wrap."""
+    q_len = 83
+    mask = oatt.block_causal_mask(q_len, cache_len, torch.tensor(starts))
+    want = torch.tensor(brute.slice_mask(q_len, cache_len, starts))
+    assert torch.equal(mask, want)
+    for i in range(0, q_len, 7):
+        for j in range(cache_len + q_len):
+            assert bool(mask[i, j]) == brute.key_visible(i, j, q_len, cache_len, starts, False)
+
+
+@pytest.mark.parametrize("cache_len", [0, 5])
+@pytest.mark.parametrize("mode", ["none", "causal", "blocks", "late_first"])
+def test_slice_mask_matches_brute_rule(cache_len, mode):
+    """The two brute restatements agree with each other on ordinary inputs."""
+    q_len = 13
+    starts = {"none": None, "causal": None, "blocks": [0, 4, 9], "late_first": [3, 8]}[mode]
+    causal = mode == "causal"
+    want = brute.slice_mask(q_len, cache_len, starts, causal)
+    for i in range(q_len):
+        for j in range(cache_len + q_len):
+            assert want[i][j] == brute.key_visible(i, j, q_len, cache_len, starts, causal)
+
+
+def test_wrapped_negative_stop_is_visible():
+    """Known answer: ``[0, -40, 83]`` over 83 queries at cache_len 0. The pair
+    (0, -40) sets rows 0..42 (``0:-40`` of 83) and columns ``0:-40``, i.e. keys
+    0..42; the pair (-40, 83) sets rows 43..82 and every key."""
+    mask = oatt.block_causal_mask(83, 0, torch.tensor([0, -40, 83]))
+    assert mask[:43, :43].all() and not mask[:43, 43:].any()
+    assert mask[43:].all()
+    # At cache_len 10 the stop 10 - 40 still wraps: current keys [0, 10 + 83 - 40).
+    mask = oatt.block_causal_mask(83, 10, torch.tensor([0, -40, 83]))
+    assert mask[:43, :10 + 53].all() and not mask[:43, 10 + 53:].any()
+    # At cache_len 39 the stop -1 wraps to the last column: all but the last key.
+    mask = oatt.block_causal_mask(83, 39, torch.tensor([0, -40, 83]))
+    assert mask[:43, :39 + 82].all() and not mask[:43, 39 + 82:].any()
+    # At cache_len 40 the stop is 0, before the slice's start: only the cache.
+    mask = oatt.block_causal_mask(83, 40, torch.tensor([0, -40, 83]))
+    assert mask[:43, :40].all() and not mask[:43, 40:].any()
+
+
+def test_slice_pin_catches_an_unwrapped_stop():
+    """A planted oracle that takes ``min(hi, q_len)`` for every pair (no wrap
+    of a negative stop) fails the slice-built mask."""
+    q_len, cache_len, starts = 83, 0, [0, -40, 83]
+    bounds = starts + [q_len]
+    end = torch.zeros(q_len, dtype=torch.int64)
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        end[lo:hi] = torch.clamp(end[lo:hi], min=min(hi, q_len))
+    planted = torch.arange(cache_len + q_len)[None, :] < (cache_len + end)[:, None]
+    assert not torch.equal(planted, torch.tensor(brute.slice_mask(q_len, cache_len, starts)))
+
+
 def test_mask_c0_structure():
     """C0: 3 blocks of 16; block b sees keys [0, 16(b+1)) exactly."""
     mask = oatt.block_causal_mask(48, 0, torch.tensor([0, 16, 32]))

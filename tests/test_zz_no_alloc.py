@@ -96,3 +96,53 @@ def test_noalloc_refuses_a_call_beyond_the_scratch(device, built_lib):
     assert "static scratch" in lib.dx_last_error().decode()
     torch.cuda.synchronize()
     assert bool((out_before == 7.0).all())
+
+
+def test_noalloc_first_call_under_graph_capture(device, built_lib, tmp_path):
+    """The entry point's first call on a device sets its scratch up (the symbol
+    lookup and a counter-clearing kernel on the caller's stream). Here that first
+    call is made under graph capture: a private copy of the library is loaded,
+    whose static scratch and per-device set-up are its own, so its first call is
+    a first call whatever ran before in this process. The graph is replayed
+    several times, with eager calls in between, and every replay must equal the
+    workspace entry point bit for bit (the one-launch decode kernel, which keeps
+    its arrival counters in the scratch)."""
+    import ctypes
+    import shutil
+
+    copy = tmp_path / "libdexter_gfx950_capture_copy.so"
+    shutil.copyfile(built_lib, copy)
+    fresh = ctypes.CDLL(str(copy))
+    for name, (res, args) in _lib._SIGNATURES.items():
+        fn = getattr(fresh, name)
+        fn.restype, fn.argtypes = res, args
+    lib = _lib.load()
+    q, k, v, cache, c = _case(device, 1, 83, 24, 128, 1245, 530)
+    b, lq, h, d = q.shape
+    with _lib.tuning(_lib.TUNE_ATTN_KERNEL, 4), _lib.tuning(_lib.TUNE_ATTN_MERGE, 1):
+        fresh.dx_set_tuning(_lib.TUNE_ATTN_KERNEL, 4)
+        fresh.dx_set_tuning(_lib.TUNE_ATTN_MERGE, 1)
+        rc, ref = _call(lib, False, q, k, v, cache, c)
+        _lib.check(rc, "attention")
+        out = torch.zeros_like(q)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        print("no-alloc: first call of a fresh library copy under capture", flush=True)
+        with torch.cuda.graph(graph, stream=s):
+            rc = fresh.dx_blockwise_causal_attention_noalloc(
+                q.data_ptr(), *_strides(q), k.data_ptr(), *_strides(k), v.data_ptr(),
+                *_strides(v), cache.data_ptr(), cache.stride(0), cache.stride(1),
+                cache.stride(2), cache.stride(3), out.data_ptr(), *_strides(out), _lib.DX_BF16,
+                b, lq, lq, h, h, d, c, None, _lib.DX_I32, 0, 0, float(d) ** -0.5, s.cuda_stream)
+        assert rc == 0, fresh.dx_last_error().decode()
+        torch.cuda.synchronize()
+        for rep in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {rep} differs from the workspace entry point"
+            rc, again = _call(lib, False, q, k, v, cache, c)  # eager work between replays
+            _lib.check(rc, "attention")
+        fresh.dx_set_tuning(_lib.TUNE_ATTN_KERNEL, 0)
+        fresh.dx_set_tuning(_lib.TUNE_ATTN_MERGE, 0)
