@@ -145,6 +145,10 @@ struct AttnArgs {
   // Time a workgroup waits for its group on the L2 fast path of the
   // in-kernel merge (s_memrealtime ticks); 0 skips the fast path.
   uint32_t fast_ticks;
+  // Dual-stream kernel, split groups merged in the launch: spread the merge
+  // over the group's splits (spread_split_group) instead of leaving it to
+  // the last one to arrive (arrive_split_group).
+  int spread;
   int seg_b[kMaxSeg], seg_splits[kMaxSeg], seg_cache[kMaxSeg];
   int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
 };
@@ -1404,6 +1408,226 @@ __device__ __forceinline__ void arrive_split_group(const AttnArgs& a, const Coor
   DX_STAMP(7);
 }
 
+// Rows [r_lo, r_lo + rn) of a split group's output, merged from the
+// row-major partials of the paired and dual-stream kernels (rn <= BM / 2: a
+// chunk of a group of at least two splits), with the merge kernel's
+// arithmetic in its order (merge_weights, merge_add2 in split order; splits
+// past the group's read as zeros and weigh 0). Thread t < rn turns row t's
+// records into the split weights (into LDS) while every thread's value loads
+// are in flight: thread t takes units (row, 8 dims: 16 bytes) t + NT k, so
+// consecutive threads read consecutive 16 bytes of a row. kAux: cache policy
+// of the loads (kScXcd: from this XCD's L2; kScDevice: from memory).
+template <int D, typename T, int BM, int NT, int kAux>
+__device__ __forceinline__ void merge_rows(const AttnArgs& a, const Coord& it, int q0, int r_lo,
+                                           int rn, uint16_t* smem) {
+  constexpr int CR = D / 8;
+  constexpr int UPT = (BM / 2 * CR + NT - 1) / NT;  // units per thread, at most
+  const int S = it.n_splits;
+  const uint32_t rows = uint32_t(a.bm);
+  const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + it.pbase * a.bm * 4, (short)0, int(uint32_t(S) * rows * 16), kBufWord3);
+  const __amdgpu_buffer_rsrc_t rval = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o + it.pbase * a.bm * D, (short)0, int(uint32_t(S) * rows * D * 2), kBufWord3);
+  float* const lc = reinterpret_cast<float*>(smem);                        // [row][split]
+  int* const le = reinterpret_cast<int*>(lc + BM / 2 * kPMergeSplits);  // [row] exponent E
+  const int t = int(threadIdx.x), nu = rn * CR;
+  u32x4 v[UPT][kPMergeSplits];
+#pragma unroll
+  for (int k = 0; k < UPT; ++k) {
+    const int u = t + NT * k;
+    // Units past the chunk read past every bound (zeros, unused).
+    const uint32_t base = u < nu ? uint32_t(r_lo + u / CR) * (D * 2) + uint32_t(u % CR) * 16
+                                 : 0x80000000u;
+#pragma unroll
+    for (int sp = 0; sp < kPMergeSplits; ++sp)
+      v[k][sp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rval, base + uint32_t(sp) * rows * (D * 2), 0, kAux));
+  }
+  if (t < rn) {
+    f32x4 ml[kPMergeSplits];
+#pragma unroll
+    for (int sp = 0; sp < kPMergeSplits; ++sp)
+      ml[sp] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rrec, (uint32_t(sp) * rows + uint32_t(r_lo + t)) * 16,
+                                             0, kAux));
+    float c[kPMergeSplits];
+    const int emax = merge_weights(ml, S, c);
+#pragma unroll
+    for (int sp = 0; sp < kPMergeSplits; ++sp) lc[t * kPMergeSplits + sp] = c[sp];
+    le[t] = emax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < UPT; ++k) {
+    const int u = t + NT * k;
+    if (u >= nu) continue;
+    const int r = u / CR, ch = u % CR;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < kPMergeSplits; ++sp) {
+      const float cs = lc[r * kPMergeSplits + sp];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) merge_add2(acc[2 * e], acc[2 * e + 1], cs, v[k][sp][e]);
+    }
+    const int emax = le[r];
+    u32x4 packed;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      packed[e] = Mfma<T>::pack(__builtin_ldexpf(acc[2 * e], emax),
+                                __builtin_ldexpf(acc[2 * e + 1], emax));
+    uint16_t* op =
+        a.out + it.b * a.o_sb + int64_t(q0 + r_lo + r) * a.o_sl + it.h * a.o_sh + ch * 8;
+    __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(op));
+  }
+  DX_STAMP(6);
+}
+
+// Wait of a split for the other splits of its group before a spread merge:
+// s_memrealtime ticks (100 MHz), 20 us, ample for co-resident workgroups;
+// reached only when a split cannot be scheduled until others leave.
+constexpr uint32_t kSpreadTicks = 2000;
+// Slow path's poll limit (50 us), as kSpinTicks of the decode kernel.
+constexpr uint64_t kSpreadSpinTicks = 5000;
+
+// Spread merge of a split group in the same launch (dual-stream kernel):
+// every split stores its partial with plain stores (into its XCD's L2),
+// arrives, and once all S splits have arrived merges row chunk c = its split
+// index (rows [c nrows / S, (c + 1) nrows / S)) of every split's partial, so
+// the group's merge is shared by its S workgroups instead of read by one.
+//
+// Arrival (thread 0). Group word w (64-bit, counters[0..1]) counts arrivals
+// in bits [0, 16), marks from bit 16, and the arrivals from XCC x in the
+// nibble at bit 32 + 4 x; counters[2] counts finished workgroups. Atomics
+// are coherent across the device; plain stores reach only the issuing XCD's
+// L2. A workgroup that sees all S arrivals and no mark, every one from its
+// own XCC, merges its chunk with loads from that L2 (kScXcd: the fast path).
+// One that does not see S arrivals within kSpreadTicks marks the word, by
+// compare-and-swap and only while arrivals < S; then, or when the arrivals
+// came from several XCCs, every workgroup of the group takes the slow path
+// (the word decides it for all alike):
+//
+// Slow path, at device scope: every split stores its partial again through
+// to memory (``restore``), then counters[4] counts arrivals, counters[5]
+// finishes and counters[6 + c] claims chunk c. A workgroup that is not the
+// last arrival polls until all have arrived, with a time limit; a chunk is
+// merged by whoever claims it first (compare-and-swap): its owner once all
+// have arrived, or the last arrival, which after its own chunk claims every
+// chunk still unclaimed. Every chunk is merged exactly once.
+//
+// The S-th workgroup to finish with each state resets it to zero, so the
+// counters are zero after every call. Every thread of the workgroup calls
+// it, after its own partial stores are issued; the LDS below ``sh_words``
+// (ints from smem) must be idle.
+template <int D, typename T, int BM, int NT, typename Restore>
+__device__ __forceinline__ void spread_split_group(const AttnArgs& a, const Coord& it, int q0,
+                                                   uint16_t* smem, Restore&& restore) {
+  static_assert(kPMergeSplits < 16, "an XCD's arrivals fit its nibble");
+  static_assert(6 + kPMergeSplits <= kCounterStride, "group state fits its slot");
+  constexpr int kShWords = BM / 2 * (kPMergeSplits + 1);  // past merge_rows' scratch
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are in the L2
+  __syncthreads();
+  const int S = it.n_splits;
+  int32_t* const fs = a.counters + it.pbase * kCounterStride;
+  uint64_t* const fw = reinterpret_cast<uint64_t*>(fs);
+  int32_t* const gs = fs + 4;
+  int* const sh = reinterpret_cast<int*>(smem) + kShWords;
+  constexpr uint64_t kMark = 1ull << 16;
+  if (threadIdx.x == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+    const uint64_t mine = 1ull | (1ull << (32 + 4 * xcc));
+    const uint64_t alone = uint64_t(S) << (32 + 4 * xcc);  // all S arrivals from this XCC
+    int fast = -1;
+    uint64_t v = __hip_atomic_fetch_add(fw, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    DX_NOTE(11, t0);  // own arrival counted
+    while (fast < 0) {
+      const uint64_t arrived = v & (kMark - 1), marks = (v >> 16) & 0xffffull;
+      if (marks != 0) {
+        fast = 0;
+      } else if (arrived == uint64_t(S)) {
+        fast = (v >> 32) == (alone >> 32) ? 1 : 0;
+      } else if (__builtin_amdgcn_s_memrealtime() - t0 > kSpreadTicks) {
+        uint64_t expect = v;
+        if (__hip_atomic_compare_exchange_strong(fw, &expect, v + kMark, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+          fast = 0;
+        else
+          v = expect;  // changed meanwhile: decide on the new value
+      } else {
+        __builtin_amdgcn_s_sleep(1);
+        v = __hip_atomic_fetch_add(fw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    sh[0] = fast;
+  }
+  __syncthreads();
+  DX_STAMP(5);
+  DX_NOTE(8, uint32_t(it.split) | uint32_t(it.n_splits) << 8 | uint32_t(it.b) << 16 |
+                 uint64_t(sh[0] ? 3 : 4) << 32);
+  const bool fast = sh[0] != 0;
+  const int nrows = min(BM, a.Lq - q0);
+  auto chunk = [&](int c, auto aux) __attribute__((always_inline)) {
+    const int r_lo = c * nrows / S;
+    merge_rows<D, T, BM, NT, decltype(aux)::value>(a, it, q0, r_lo, (c + 1) * nrows / S - r_lo,
+                                                   smem);
+  };
+  if (fast) {
+    chunk(it.split, std::integral_constant<int, kScXcd>{});
+  } else {
+    restore();  // the partial again, through to memory
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int prev = __hip_atomic_fetch_add(gs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == S - 1;
+      int all = last;
+      if (!last) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+          if (__hip_atomic_fetch_add(gs, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= S) {
+            all = 1;
+            break;
+          }
+          if (__builtin_amdgcn_s_memrealtime() - t0 > kSpreadSpinTicks) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      sh[1] = all;
+      sh[2] = last;
+    }
+    __syncthreads();
+    const bool all = sh[1] != 0, last = sh[2] != 0;
+    for (int c0 = 0; all && c0 < (last ? S : 1); ++c0) {
+      const int c = it.split + c0 < S ? it.split + c0 : it.split + c0 - S;  // own chunk first
+      __syncthreads();  // the previous chunk's LDS scratch and sh[3] have been read
+      if (threadIdx.x == 0) {
+        int unclaimed = 0;
+        sh[3] = __hip_atomic_compare_exchange_strong(gs + 2 + c, &unclaimed, 1, __ATOMIC_RELAXED,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!sh[3]) continue;
+      chunk(c, std::integral_constant<int, kScDevice>{});
+    }
+    if (threadIdx.x == 0) {
+      // Done with the slow state; the last to get here resets it.
+      if (__hip_atomic_fetch_add(gs + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1) {
+        for (int i = 0; i < 2 + S; ++i)
+          __hip_atomic_store(gs + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (threadIdx.x == 0) {
+    // Done with the arrival state; the S-th to finish resets it.
+    if (__hip_atomic_fetch_add(fs + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1) {
+      __hip_atomic_store(fw, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(fs + 2, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  DX_STAMP(7);
+}
+
 // The dual-stream kernel's results after its split hand-over: stream s holds
 // head_dim blocks [s DT / 2, (s + 1) DT / 2) of its wave's 32 rows (r0 ..)
 // and the whole row's (l_tot, mref). Both streams pack their blocks into the
@@ -1415,7 +1639,7 @@ __device__ __forceinline__ void arrive_split_group(const AttnArgs& a, const Coor
 // The stream is a template parameter so that every block index is a constant
 // (a register array indexed at run time would live in scratch memory).
 template <int D, typename T, int stream, int kAux = 0>
-__device__ __forceinline__ void store_result_halves(const AttnArgs& a, const Coord& it, int q0,
+__device__ __forceinline__ int store_result_halves(const AttnArgs& a, const Coord& it, int q0,
                                                     int r0, int g, int lane, int ltid,
                                                     bool active,
                                                     const f32x16 (&acc)[D / 32], float l_tot,
@@ -1475,7 +1699,7 @@ __device__ __forceinline__ void store_result_halves(const AttnArgs& a, const Coo
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's blocks are in LDS
   __syncthreads();                     // both streams' blocks of every row
-  if (!active) return;
+  if (!active) return e;
   const int rs = r0 + 16 * stream;     // this stream stores rows rs .. rs + 15
   const int nr = min(nrows - 16 * stream, 16);
   __amdgpu_buffer_rsrc_t ro;
@@ -1489,6 +1713,32 @@ __device__ __forceinline__ void store_result_halves(const AttnArgs& a, const Coo
     ro = make_rsrc(a.ws_o + ((it.pbase + it.split) * a.bm + rs) * D, max(nr, 0), ro_bytes, D);
   }
   A::template store_rows<kAux, 16>(ro, ro_bytes, nr, area, rs, lane);
+  return e;
+}
+
+// The partial that store_result_halves stored (a split work item), stored
+// again through to memory (kScDevice): the rows from the row area, which
+// still holds them, and the records from the values it was given.
+template <int D, int stream>
+__device__ __forceinline__ void restore_partial_halves(const AttnArgs& a, const Coord& it, int q0,
+                                                       int r0, int g, int lane, bool active,
+                                                       float l_tot, float mref, int e,
+                                                       uint32_t area) {
+  if (!active) return;
+  const int row = r0 + (lane & 31);
+  const int nrows = min(a.Lq - q0 - r0, 32);
+  const int64_t pidx = it.pbase + it.split;
+  if (stream == 0 && g == 0 && row - r0 < nrows)
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(u32x4, f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(e), 0.f}),
+        __builtin_amdgcn_make_buffer_rsrc(a.ws_ml + pidx * a.bm * 4, (short)0, a.bm * 16,
+                                          kBufWord3),
+        row * 16, 0, kScDevice);
+  const int rs = r0 + 16 * stream;
+  const int nr = min(nrows - 16 * stream, 16);
+  RowArea<D>::template store_rows<kScDevice, 16>(
+      make_rsrc(a.ws_o + (pidx * a.bm + rs) * D, max(nr, 0), D * 2, D), D * 2, nr, area, rs,
+      lane);
 }
 
 template <int D, typename T, int NS>
@@ -1774,13 +2024,27 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
         DX_STAMP(7);
         return;
       }
+      static_assert((kBM * (kPMergeSplits + 1) + 4) * 4 <= Lds<D>::bytes,
+                    "merge scratch below the row area");
+      if (a.spread) {
+        // Split, merged in this launch and spread over the group
+        // (spread_split_group): the partial goes to this XCD's L2; every
+        // split then merges its chunk of rows once the group has arrived.
+        const int e = store_result_halves<D, T, S>(a, it, q0, wave * 32, g, lane, ltid,
+                                                   wave_active, acc, l_tot, mref, area, ax);
+        DX_STAMP(4);
+        spread_split_group<D, T, kBM, 64 * kNW * NS>(
+            a, it, q0, smem, [&]() __attribute__((always_inline)) {
+              restore_partial_halves<D, S>(a, it, q0, wave * 32, g, lane, wave_active, l_tot,
+                                           mref, e, area);
+            });
+        return;
+      }
       // Split, merged in this launch: store the partial, then every wave
       // arrives (arrive_split_group); the last split of the group merges.
       store_result_halves<D, T, S, kScDevice>(a, it, q0, wave * 32, g, lane, ltid, wave_active,
                                               acc, l_tot, mref, area, ax);
       DX_STAMP(4);
-      static_assert((kBM * (kPMergeSplits + 1) + 1) * 4 <= Lds<D>::bytes,
-                    "merge scratch below the row area");
       arrive_split_group<D, T, kBM, 64 * kNW * NS, 2>(a, it, q0, smem);
     };
     if (stream == 0) epilogue(std::integral_constant<int, 0>{});
@@ -2992,6 +3256,7 @@ struct Plan {
   int64_t items, comb_blocks, partials;
   int64_t counter_bytes;     // arrival counters at the start of the workspace
   bool pmerge;               // splits merged in the kernel (no merge launch)
+  bool spread;               // ... spread over each group's splits (dual-stream kernel)
   int64_t ws_bytes;
 };
 
@@ -3239,12 +3504,19 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   // the merge lies on the critical path: at C1 (8 splits of 83 rows) one
   // workgroup's merge of 170 KB of partials took longer than the merge kernel,
   // 14.7 vs 12.7 us per call.
+  // The dual-stream kernel can also spread the merge over each group's splits
+  // (spread_split_group, DX_TUNE_ATTN_PMERGE 3): every split waits for its
+  // group, then merges its own chunk of rows from the L2. At C1 that measured
+  // 13.39 us per call against 12.55 us with the merge kernel (14.27 us with
+  // the last split merging), so it is not the default.
   int most = p.uniform_splits;
   for (int sk : p.seg_splits) most = std::max(most, sk);
   const int pm = tuning(DX_TUNE_ATTN_PMERGE);
+  const bool fits = has_partials && most <= kPMergeSplits && p.partials <= kCounterSlots;
   const bool in_launch = p.kernel == kPaired || (p.kernel == kDual && p.n_seg > 0);
-  p.pmerge = (pm == 2 ? p.kernel == kPaired || p.kernel == kDual : pm == 0 && in_launch) &&
-             has_partials && most <= kPMergeSplits && p.partials <= kCounterSlots;
+  p.pmerge = fits && (pm == 2 || pm == 3 ? p.kernel == kPaired || p.kernel == kDual
+                                         : pm == 0 && in_launch);
+  p.spread = p.pmerge && p.kernel == kDual && pm == 3;
   if (p.pmerge) p.comb_blocks = 0;
   return p;
 }
@@ -3317,6 +3589,7 @@ hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 
 // Static scratch of the no-allocation entry point: one copy per device,
 // holding the layout a caller's workspace does ([counters][partial values]
@@ -3468,6 +3741,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                    ? reinterpret_cast<int32_t*>(ws)
                    : nullptr;
   a.fast_ticks = tuning(DX_TUNE_ATTN_MERGE) == 2 ? 0u : kFastTicks;
+  a.spread = a.counters != nullptr && p.spread;
   a.ws_o = p.ws_bytes ? reinterpret_cast<uint16_t*>(ws + p.counter_bytes) : nullptr;
   a.ws_ml = p.ws_bytes ? reinterpret_cast<float*>(a.ws_o + p.partials * p.prow * D) : nullptr;
   a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
@@ -3512,10 +3786,72 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   return DX_OK;
 }
 
+// QK-norm + rotary prologue (with the cache write when appending), then
+// attention over the cache and the rotated rows: SelfAttention's decode step
+// in one call. The prologue stays its own kernel: run inside the attention
+// launch (the first workgroups normalising the tokens while the others fetch
+// cache tiles, the attention waiting for them before reading q) it measured
+// 4.4 us slower per call at every cache length from 1,245 to 32,768 keys, since
+// q is needed before the first tile and the in-launch hand-over costs three
+// dependent memory round trips under load.
+int fused_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k,
+                int64_t k_sb, int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb,
+                int64_t v_sl, int64_t v_sh, int io_dtype, const void* qw, const void* kw,
+                int wdt, const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl,
+                int tdt, float eps, int interleaved, void* q_out, void* k_out, void* cache,
+                int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh, int64_t capacity,
+                int64_t cache_len, int append, void* out, int64_t o_sb, int64_t o_sl,
+                int64_t o_sh, int64_t B, int64_t L, int64_t H, int64_t D, const void* starts,
+                int starts_dtype, int64_t n_blocks, int causal, float softmax_scale,
+                void* workspace, int64_t ws_bytes, void* stream) {
+  DX_CHECK_ARG(cache_len >= 0, "qk_norm_rope_attention: negative cache_len");
+  DX_CHECK_ARG(D == 64 || D == 128, "qk_norm_rope_attention: head_dim %lld unsupported (64 or "
+               "128)", (long long)D);
+  int rc = rope_validate(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, io_dtype,
+                         qw, kw, wdt, cos, cos_sl, sin, sin_sl, tdt, q_out, k_out, cache,
+                         c_plane, c_sb, c_ss, c_sh, capacity, cache_len, nullptr, B, L, H, D,
+                         append != 0);
+  if (rc) return rc;
+  DX_CHECK_ARG(cache_len == 0 || cache, "qk_norm_rope_attention: cache_len > 0 needs a cache");
+  if (B * L == 0) return DX_OK;
+  rc = append ? dx_qk_norm_rope_append(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl,
+                                       v_sh, io_dtype, qw, kw, wdt, cos, cos_sl, sin, sin_sl,
+                                       tdt, q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh,
+                                       capacity, cache_len, B, L, H, D, eps, interleaved, stream)
+              : dx_qk_norm_rope(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, io_dtype, qw, kw, wdt,
+                                cos, cos_sl, sin, sin_sl, tdt, q_out, k_out, B, L, H, D, eps,
+                                interleaved, stream);
+  if (rc) return rc;
+  // The rotated q and k are [B, L, H, D], contiguous (stride 0 for a size-1 dim).
+  const int64_t hd = H * D, sb = B == 1 ? 0 : L * hd, sl = L == 1 ? 0 : hd;
+  return attention_entry(q_out, sb, sl, D, k_out, sb, sl, D, v, v_sb, v_sl, v_sh, cache,
+                         c_plane, c_sb, c_ss, c_sh, out, o_sb, o_sl, o_sh, io_dtype, B, L, L, H,
+                         H, D, cache_len, nullptr, nullptr, starts, starts_dtype, n_blocks,
+                         causal, softmax_scale, workspace, ws_bytes, stream);
+}
+
 }  // namespace
 }  // namespace dx
 
 using namespace dx;
+
+extern "C" int dx_qk_norm_rope_attention(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k, int64_t k_sb,
+    int64_t k_sl, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    int io_dtype, const void* q_weight, const void* k_weight, int weight_dtype,
+    const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl, int table_dtype,
+    float eps, int interleaved, void* q_out, void* k_out, void* cache, int64_t c_plane,
+    int64_t c_sb, int64_t c_ss, int64_t c_sh, int64_t capacity, int64_t cache_len, int append,
+    void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh, int64_t B, int64_t L, int64_t H,
+    int64_t D, const void* block_starts, int starts_dtype, int64_t n_blocks, int causal,
+    float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  return fused_entry(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh, io_dtype,
+                     q_weight, k_weight, weight_dtype, cos, cos_sl, sin, sin_sl, table_dtype, eps,
+                     interleaved, q_out, k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity,
+                     cache_len, append, out, o_sb, o_sl, o_sh, B, L, H, D, block_starts,
+                     starts_dtype, n_blocks, causal, softmax_scale, workspace, workspace_bytes,
+                     stream);
+}
 
 extern "C" int dx_blockwise_causal_attention(
     const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, const void* k, int64_t k_sb,

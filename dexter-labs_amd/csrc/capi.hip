@@ -34,8 +34,9 @@ extern "C" int dx_abi_version(void) { return DX_ABI_VERSION; }
 
 extern "C" int dx_set_tuning(int key, int value) {
   // Largest value per key: splits 16, attention kernel 4, norm waves 16,
-  // QKV splits 16, QKV waves 4, decode merge 2, prefill merge 2.
-  static const int kMax[DX_TUNE_KEYS] = {16, 4, 16, 16, 4, 2, 2};
+  // QKV splits 16, QKV waves 4, decode merge 2, split merge of the paired
+  // and dual-stream kernels 3.
+  static const int kMax[DX_TUNE_KEYS] = {16, 4, 16, 16, 4, 2, 3};
   DX_CHECK_ARG(key >= 0 && key < DX_TUNE_KEYS, "set_tuning: unknown key %d", key);
   DX_CHECK_ARG(value >= 0 && value <= kMax[key], "set_tuning: value %d out of range for key %d",
                value, key);

@@ -47,10 +47,45 @@ template <> struct Store<f16_t> {
   static __device__ __forceinline__ uint16_t bits(float f) { return f32_to_f16_bits(f); }
 };
 
+// The fp32 value as computed, hidden from the optimizer, so that the rounding
+// to a 16-bit type that follows is a rounding of this fp32 value: otherwise
+// an fp32 product or sum and its conversion to f16 may become one
+// mixed-precision instruction (one rounding where the reference rounds
+// twice), and not alike in every kernel that inlines the same code.
+__device__ __forceinline__ float held(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Pack two floats into one dword of 16-bit values (lo in bits 0..15).
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return uint32_t(Store<T>::bits(lo)) | (uint32_t(Store<T>::bits(hi)) << 16);
+}
+
+// Sum over the 64 lanes of a wave, the same bits on every lane, by VALU lane
+// exchanges instead of LDS permutes: DPP within each row of 16 lanes (lanes
+// i ^ 1, i ^ 2, then the half-row and row mirrors), then the gfx950 row swaps
+// (lanes i ^ 16, i ^ 32). Every step adds a lane's value to its partner's,
+// and the partner adds the same two values, so all lanes agree. (The QK-norm
+// prologue's sum of squares, in its own kernel and inside the decode
+// attention launch, so that both round alike.)
+template <int kCtrl>
+__device__ __forceinline__ float dpp_add(float x) {
+  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf,
+                                                        false));
+}
+__device__ __forceinline__ float lane_sum64(float x) {
+  x = dpp_add<0xb1>(x);   // quad_perm [1, 0, 3, 2]: lane i ^ 1
+  x = dpp_add<0x4e>(x);   // quad_perm [2, 3, 0, 1]: lane i ^ 2
+  x = dpp_add<0x141>(x);  // row_half_mirror: lane 7 - i within 8
+  x = dpp_add<0x140>(x);  // row_mirror: lane 15 - i within 16
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                    false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
 }  // namespace dx
@@ -63,6 +98,16 @@ namespace dx {
 void set_error(const char* fmt, ...);
 // Current value of a dx_set_tuning override (0: the library's own choice).
 int tuning(int key);
+// Argument checks of the QK-norm + rotary prologue (qk_norm_rope.hip), also
+// run by the attention launch that does the prologue itself.
+int rope_validate(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                  const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                  const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh, int io_dtype,
+                  const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
+                  const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
+                  void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                  int64_t capacity, int64_t start, const int32_t* start_dev,
+                  int64_t B, int64_t L, int64_t H, int64_t D, bool append);
 }
 
 #define DX_CHECK_ARG(cond, ...)                   \

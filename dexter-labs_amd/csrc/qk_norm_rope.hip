@@ -179,29 +179,6 @@ __device__ __forceinline__ void projected(const RopeArgs& a, const float* row, i
   }
 }
 
-// Sum over the 64 lanes of a wave, the same bits on every lane, by VALU lane
-// exchanges instead of LDS permutes: DPP within each row of 16 lanes (lanes
-// i ^ 1, i ^ 2, then the half-row and row mirrors), then the gfx950 row swaps
-// (lanes i ^ 16, i ^ 32). Every step adds a lane's value to its partner's,
-// and the partner adds the same two values, so all lanes agree.
-template <int kCtrl>
-__device__ __forceinline__ float dpp_add(float x) {
-  return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf,
-                                                        false));
-}
-__device__ __forceinline__ float wave_sum(float x) {
-  x = dpp_add<0xb1>(x);   // quad_perm [1, 0, 3, 2]: lane i ^ 1
-  x = dpp_add<0x4e>(x);   // quad_perm [2, 3, 0, 1]: lane i ^ 2
-  x = dpp_add<0x141>(x);  // row_half_mirror: lane 7 - i within 8
-  x = dpp_add<0x140>(x);  // row_mirror: lane 15 - i within 16
-  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
-                                                    false, false);
-  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
-                                                    false, false);
-  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-}
-
 // Cache slot of this call: the host start, or the device start row when one is
 // given (then a block that would not fit is skipped and flagged in *status).
 __device__ __forceinline__ bool cache_start(const RopeArgs& a, bool flag, int64_t& start) {
@@ -223,6 +200,11 @@ __device__ __forceinline__ bool cache_start(const RopeArgs& a, bool flag, int64_
 template <typename IO, typename W, typename TB, bool INTERLEAVED, bool APPEND, bool PROJ,
           int kThreads>
 __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
+  // Every product and sum rounded on its own, as the reference's tensor ops
+  // round them (rope.py:20-26, :36-40): otherwise the compiler may fuse a
+  // rotation product into its sum (one rounding), which near cancellation
+  // changes the result, and differently in each kernel that inlines this.
+#pragma clang fp contract(off)
   prefetch_args(a);
   __shared__ float red[kThreads / 64];
   // Grid (L, planes, B): no division to find the token.
@@ -294,15 +276,15 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sq += x[p][e] * x[p][e];
-  sq = wave_sum(active ? sq : 0.f);
+    for (int e = 0; e < 8; ++e) sq = __builtin_fmaf(x[p][e], x[p][e], sq);
+  sq = lane_sum64(active ? sq : 0.f);
   const int wave = threadIdx.x >> 6, n_waves = blockDim.x >> 6;
   if ((threadIdx.x & 63) == 0) red[wave] = sq;
   __syncthreads();
   if (!active) return;
   float t = 0.f;
   for (int w = 0; w < n_waves; ++w) t += red[w];
-  const float rr = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(t, float(hd)) + a.eps));
+  const float rr = 1.0f / __builtin_sqrtf(t / float(hd) + a.eps);
 
   // ---- norm (rounded to io, as _rms does), then rotation ------------------
   float fw[2][8], c[8], s[8];
@@ -313,7 +295,7 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[p][e] = round_io<IO>(__fmul_rn(__fmul_rn(x[p][e], rr), fw[p][e]));
+    for (int e = 0; e < 8; ++e) x[p][e] = round_io<IO>(held((x[p][e] * rr) * fw[p][e]));
   float o[2][8];
 #pragma unroll
   for (int t8 = 0; t8 < 8; ++t8) {
@@ -323,8 +305,8 @@ __device__ __forceinline__ void prologue_body(const RopeArgs& a) {
     const int p_lo = INTERLEAVED ? t8 / 4 : 0, e_lo = INTERLEAVED ? 2 * (t8 % 4) : t8;
     const int p_hi = INTERLEAVED ? t8 / 4 : 1, e_hi = INTERLEAVED ? 2 * (t8 % 4) + 1 : t8;
     const float xl = x[p_lo][e_lo], xh = x[p_hi][e_hi];
-    o[p_lo][e_lo] = __fsub_rn(__fmul_rn(xl, c[t8]), __fmul_rn(xh, s[t8]));
-    o[p_hi][e_hi] = __fadd_rn(__fmul_rn(xl, s[t8]), __fmul_rn(xh, c[t8]));
+    o[p_lo][e_lo] = held(xl * c[t8] - xh * s[t8]);
+    o[p_hi][e_hi] = held(xl * s[t8] + xh * c[t8]);
   }
   u32x4 po[2];
 #pragma unroll
@@ -438,15 +420,17 @@ int check_common(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
 
 using namespace dx;
 
-static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
-                      const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
-                      const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh, int io_dtype,
-                      const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
-                      const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
-                      void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
-                      int64_t capacity, int64_t start, const int32_t* start_dev,
-                      int32_t* status, int64_t B, int64_t L, int64_t H,
-                      int64_t D, float eps, int interleaved, void* stream, bool append) {
+namespace dx {
+// The prologue's argument checks, shared with the decode attention launch
+// that runs the prologue itself (dx_qk_norm_rope_attention).
+int rope_validate(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                  const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                  const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh, int io_dtype,
+                  const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
+                  const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
+                  void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                  int64_t capacity, int64_t start, const int32_t* start_dev,
+                  int64_t B, int64_t L, int64_t H, int64_t D, bool append) {
   int rc = check_common(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, io_dtype, qw, kw, wdt, cos,
                         cos_sl, sin, sin_sl, tdt, q_out, k_out, B, L, H, D);
   if (rc) return rc;
@@ -466,6 +450,24 @@ static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
                  "qk_norm_rope_append: cache/v must be 16-byte aligned with strides "
                  "that are multiples of 8 elements");
   }
+  return DX_OK;
+}
+}  // namespace dx
+
+static int rope_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+                      const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+                      const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh, int io_dtype,
+                      const void* qw, const void* kw, int wdt, const void* cos, int64_t cos_sl,
+                      const void* sin, int64_t sin_sl, int tdt, void* q_out, void* k_out,
+                      void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+                      int64_t capacity, int64_t start, const int32_t* start_dev,
+                      int32_t* status, int64_t B, int64_t L, int64_t H,
+                      int64_t D, float eps, int interleaved, void* stream, bool append) {
+  const int rc = dx::rope_validate(q, q_sb, q_sl, q_sh, k, k_sb, k_sl, k_sh, v, v_sb, v_sl, v_sh,
+                                   io_dtype, qw, kw, wdt, cos, cos_sl, sin, sin_sl, tdt, q_out,
+                                   k_out, cache, c_plane, c_sb, c_ss, c_sh, capacity, start,
+                                   start_dev, B, L, H, D, append);
+  if (rc) return rc;
   if (B * L == 0) return DX_OK;
   RopeArgs a{};
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_sb; a.q_sl = q_sl; a.q_sh = q_sh;

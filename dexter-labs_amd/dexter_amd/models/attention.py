@@ -11,7 +11,9 @@ With ``write=True`` the prologue and the append run as one kernel
 (``KVCache.append_fused``). For decode chunks (at most 128 tokens, ``dim`` a
 multiple of 512) the q/k/v projections join them: ``ops.qkv_norm_rope`` runs
 the projections, the prologue and the cache write in two kernels. Longer
-chunks use ``torch.nn.functional.linear`` (hipBLASLt) for the projections.
+chunks use ``torch.nn.functional.linear`` (hipBLASLt) for the projections and,
+with a host cache length, ``ops.qk_norm_rope_attention`` for the prologue,
+append and attention in one call.
 """
 
 from __future__ import annotations
@@ -66,6 +68,15 @@ class SelfAttention(nn.Module):
         q = F.linear(x, self.q.weight, self.q.bias).view(shape)
         k = F.linear(x, self.k.weight, self.k.bias).view(shape)
         v = F.linear(x, self.v.weight, self.v.bias).view(shape)
+        if fused_append and not isinstance(cache_len, torch.Tensor):
+            if append:
+                kv_cache._check_room(seq)
+            out = ops.qk_norm_rope_attention(
+                q, k, v, self.q_norm, self.k_norm, cos, sin,
+                kv_cache=kv_cache.cache[layer] if kv_cache is not None else None,
+                cache_len=cache_len, append=append, block_boundaries=block_boundaries,
+                eps=self.eps)
+            return F.linear(out.reshape(b, seq, -1), self.o.weight, self.o.bias)
         if append and fused_append:
             q, k = kv_cache.append_fused(layer, q, k, v, self.q_norm, self.k_norm, cos, sin,
                                          self.eps)

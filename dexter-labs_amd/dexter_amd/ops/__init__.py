@@ -14,6 +14,10 @@ and calls it, exactly as dexter's dispatchers do (``python/dexter/ops/__init__.p
   (no dispatcher in the reference: ``SelfAttention.forward`` runs three
   ``nn.Linear`` and ``ops.qk_norm_rope``, ``models/dreamzero/model.py:162-175``;
   here one call for decode chunks)
+* ``qk_norm_rope_attention``     -> ``select("attention", "qk_norm_rope_blockwise_causal", q, k, v)``
+  (no dispatcher in the reference: ``SelfAttention.forward`` calls
+  ``ops.qk_norm_rope``, ``KVCache.append`` and ``ops.blockwise_causal_attention``,
+  ``models/dreamzero/model.py:166-182``; here one call)
 * ``adaln_modulate``             -> ``select("norm", "adaln", x, scale, shift)``
   (reference ``ops/__init__.py:39-49``; same arguments and default eps)
 * ``gated_residual``             -> ``select("norm", "gated_residual", x, y, gate)``
@@ -32,7 +36,7 @@ from ..registry import select
 
 __all__ = ["qk_norm_rope", "blockwise_causal_attention", "kv_cache_append",
            "qk_norm_rope_append", "blockwise_causal_attention_varlen",
-           "adaln_modulate", "gated_residual", "qkv_norm_rope"]
+           "adaln_modulate", "gated_residual", "qkv_norm_rope", "qk_norm_rope_attention"]
 
 
 def qkv_norm_rope(
@@ -131,6 +135,40 @@ def blockwise_causal_attention(
     """
     return select("attention", "blockwise_causal", q, k, v)(
         q, k, v, kv_cache, cache_len, block_boundaries, softmax_scale, causal)
+
+
+def qk_norm_rope_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    *,
+    kv_cache: torch.Tensor | None = None,
+    cache_len: int = 0,
+    append: bool = False,
+    block_boundaries: torch.Tensor | None = None,
+    softmax_scale: float | None = None,
+    causal: bool = False,
+    eps: float = 1e-6,
+    interleaved: bool = True,
+    return_qk: bool = False,
+):
+    """``qk_norm_rope``, the cache write of the rotated k and v (``append``), and
+    ``blockwise_causal_attention``, as ``SelfAttention.forward`` chains them.
+
+    Same results as ``qr, kr = qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps,
+    interleaved)``, then (with ``append``) ``kv_cache_append(kv_cache, kr, v, cache_len)``,
+    then ``blockwise_causal_attention(qr, kr, v, kv_cache=kv_cache, cache_len=cache_len,
+    ...)``. Returns the attention output, and with ``return_qk`` also ``qr`` and ``kr``.
+    ``cache_len`` is the row count before the append (the model reads it first).
+    """
+    out, qr, kr = select("attention", "qk_norm_rope_blockwise_causal", q, k, v)(
+        q, k, v, q_weight, k_weight, cos, sin, kv_cache, cache_len, append, block_boundaries,
+        softmax_scale, causal, eps, interleaved)
+    return (out, qr, kr) if return_qk else out
 
 
 def blockwise_causal_attention_varlen(

@@ -19,4 +19,4 @@ package registers the implementations; it does not load the library, so
 registration works on any machine and only a call on a gfx950 needs it.
 """
 
-from . import attention, cache, norm, proj, rope  # noqa: F401
+from . import attention, cache, fused, norm, proj, rope  # noqa: F401

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libdexter_gfx950.so"
 LIB_PATH = Path(__file__).resolve().parents[2] / LIB_NAME
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DX_OK, DX_EINVAL, DX_ELAUNCH, DX_EFULL, DX_EWORKSPACE = 0, 1, 2, 3, 4
 DX_BF16, DX_F16, DX_F32, DX_I32, DX_I64 = 0, 1, 2, 3, 4
@@ -71,6 +71,22 @@ _SIGNATURES: dict[str, tuple[type, list]] = {
         _p, _l, _l, _l,            # out
         _i, _l, _l, _l, _l, _l, _l,  # dtype, B, Lq, Lk, H, Hkv, D
         _l, _p, _i, _l,            # cache_len, starts, starts dtype, n_blocks
+        _i, _f,                    # causal, scale
+        _p, _l, _p]),              # workspace, bytes, stream
+    "dx_qk_norm_rope_attention": (_i, [
+        _p, _l, _l, _l,            # q (pre-norm)
+        _p, _l, _l, _l,            # k (pre-norm)
+        _p, _l, _l, _l,            # v
+        _i,                        # io dtype
+        _p, _p, _i,                # q_weight, k_weight, weight dtype
+        _p, _l, _p, _l, _i,        # cos, cos_sl, sin, sin_sl, table dtype
+        _f, _i,                    # eps, interleaved
+        _p, _p,                    # q_out, k_out
+        _p, _l, _l, _l, _l,        # cache, plane, sb, ss, sh
+        _l, _l, _i,                # capacity, cache_len, append
+        _p, _l, _l, _l,            # out
+        _l, _l, _l, _l,            # B, L, H, D
+        _p, _i, _l,                # starts, starts dtype, n_blocks
         _i, _f,                    # causal, scale
         _p, _l, _p]),              # workspace, bytes, stream
     "dx_blockwise_causal_attention_noalloc": (_i, [

@@ -76,7 +76,7 @@ const char* dx_last_error(void);
 
 /* ABI revision of this header; the Python loader checks it. */
 int dx_abi_version(void);
-#define DX_ABI_VERSION 9
+#define DX_ABI_VERSION 10
 
 /*
  * Launch-schedule overrides, for measurement and tests only: process-wide,
@@ -96,9 +96,12 @@ int dx_abi_version(void);
  *   DX_TUNE_ATTN_PMERGE  key splits of the paired and dual-stream kernels:
  *                        1 merged by a separate merge kernel, 2 in the same
  *                        launch (the last split of each query tile to finish
- *                        merges all of its partials). Default: in the
- *                        launch for the paired kernel and for ragged batches
- *                        on the dual-stream kernel, else the merge kernel
+ *                        merges all of its partials), 3 in the same launch
+ *                        spread over the splits (dual-stream kernel: each
+ *                        split merges a chunk of the rows once its group has
+ *                        arrived; the paired kernel takes 2). Default: 2
+ *                        for the paired kernel and for ragged batches on the
+ *                        dual-stream kernel, else 1
  * Returns DX_EINVAL for an unknown key or an out-of-range value.
  * No reference counterpart (the reference's tuning is Triton's autotuner).
  */
@@ -257,6 +260,35 @@ int dx_blockwise_causal_attention_varlen(
     const int64_t* cache_lens, const void* block_starts, int starts_dtype,
     int64_t n_blocks, int causal, float softmax_scale,
     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * SelfAttention's decode step in one call: the QK-RMSNorm + rotary prologue
+ * of dx_qk_norm_rope (q_out, k_out written [B, L, H, D] contiguous, 16-byte
+ * aligned), with append != 0 also the cache write of dx_qk_norm_rope_append
+ * (rotated k and v into rows [cache_len, cache_len + L); DX_EFULL when
+ * cache_len + L > capacity), then dx_blockwise_causal_attention of q_out over
+ * the cache's first cache_len rows and k_out, v (Lq = Lk = L, H = Hkv).
+ * Arguments as in those entry points; workspace: dx_attention_workspace_bytes
+ * (B, L, L, H, D, cache_len, NULL) bytes, under the same zero-counter rule.
+ * Two launches (the prologue kernel, then attention) behind one call: q_out,
+ * k_out, the cache rows and out are the same bits as dx_qk_norm_rope(_append)
+ * followed by dx_blockwise_causal_attention.
+ * Replaces: models/dreamzero/model.py:166-182 (SelfAttention.forward's
+ * ops.qk_norm_rope, kv_cache.append and ops.blockwise_causal_attention).
+ */
+int dx_qk_norm_rope_attention(
+    const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh,
+    const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
+    const void* v, int64_t v_sb, int64_t v_sl, int64_t v_sh,
+    int io_dtype, const void* q_weight, const void* k_weight, int weight_dtype,
+    const void* cos, int64_t cos_sl, const void* sin, int64_t sin_sl, int table_dtype,
+    float eps, int interleaved, void* q_out, void* k_out,
+    void* cache, int64_t c_plane, int64_t c_sb, int64_t c_ss, int64_t c_sh,
+    int64_t capacity, int64_t cache_len, int append,
+    void* out, int64_t o_sb, int64_t o_sl, int64_t o_sh,
+    int64_t B, int64_t L, int64_t H, int64_t D,
+    const void* block_starts, int starts_dtype, int64_t n_blocks, int causal,
+    float softmax_scale, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Device-cursor forms. The cache row count (attention) or start row (appends)

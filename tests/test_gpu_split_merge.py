@@ -3,10 +3,12 @@ prefill kernel and the dual-stream decode kernel.
 
 With key splits, each split of a (batch, head, query tile) group leaves a
 partial output. Under ``DX_TUNE_ATTN_PMERGE`` 2 the split of the group that
-finishes last merges them all in the same launch (the paired kernel's default;
-the dual-stream kernel's only when forced), and under 1 the separate merge
-kernel does (the dual-stream kernel's default, and every kernel's for groups
-of more than eight splits). Both merges add the splits' terms in the same order with the same
+finishes last merges them all in the same launch (the paired kernel's default,
+and the dual-stream kernel's on ragged batches); under 3 every split of the
+group waits for the others and merges a chunk of the rows (dual-stream
+kernel), from its XCD's L2 when the group shares one, else at device scope;
+and under 1 the separate merge kernel does (the dual-stream kernel's default
+on uniform calls, and every kernel's for groups of more than eight splits). Both merges add the splits' terms in the same order with the same
 arithmetic, so their outputs must agree bit for bit; the merged result is also
 held to the north-star bar against the oracle
 (``python/dexter/ops/reference/attention.py:71-77``). The arrival counters
@@ -28,9 +30,11 @@ from _util import assert_parity
 
 pytestmark = pytest.mark.gpu
 
-IN_KERNEL, MERGE_KERNEL = 2, 1
-# DX_TUNE_ATTN_KERNEL values of the kernels that merge in the launch.
-KERNELS = [("paired", 3), ("dual", 2)]
+MERGE_KERNEL = 1
+# (name, DX_TUNE_ATTN_KERNEL, DX_TUNE_ATTN_PMERGE) of the in-launch merges:
+# the last split of a group merges it (2) on the paired and dual-stream
+# kernels, or every split merges a chunk of its rows (3, dual-stream).
+KERNELS = [("paired", 3, 2), ("dual", 2, 2), ("dual-spread", 2, 3)]
 
 
 def _rand(shape, device, dtype=torch.bfloat16, seed=0):
@@ -75,7 +79,7 @@ def test_in_kernel_merge_matches_merge_kernel(device, built_lib, kernel, shape, 
     def call():
         return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
 
-    got = _run(call, kernel[1], IN_KERNEL, splits)
+    got = _run(call, kernel[1], kernel[2], splits)
     ref = _run(call, kernel[1], MERGE_KERNEL, splits)
     assert torch.equal(got, ref), f"{kernel[0]} splits={splits}: in-kernel merge differs"
     if dt == torch.bfloat16:
@@ -85,11 +89,11 @@ def test_in_kernel_merge_matches_merge_kernel(device, built_lib, kernel, shape, 
 @pytest.mark.parametrize("kernel", KERNELS, ids=[k[0] for k in KERNELS])
 def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib, kernel):
     """No cache and no mask (cross-attention), then a block list over a cache."""
-    kern = kernel[1]
+    kern, in_kernel = kernel[1], kernel[2]
     q = _rand((2, 300, 4, 128), device, seed=410)
     k, v = _rand((2, 700, 4, 128), device, seed=411), _rand((2, 700, 4, 128), device, seed=412)
     for splits in (2, 4, 7):
-        got = _run(lambda: ops.blockwise_causal_attention(q, k, v), kern, IN_KERNEL, splits)
+        got = _run(lambda: ops.blockwise_causal_attention(q, k, v), kern, in_kernel, splits)
         ref = _run(lambda: ops.blockwise_causal_attention(q, k, v), kern, MERGE_KERNEL, splits)
         assert torch.equal(got, ref), f"cross splits={splits}"
         assert_parity(got, _oracle(q, k, v, None, 0), what=f"cross splits={splits}")
@@ -101,7 +105,7 @@ def test_in_kernel_merge_cross_attention_and_blocks(device, built_lib, kernel):
         return ops.blockwise_causal_attention(q, kn, vn, kv_cache=cache, cache_len=700,
                                               block_boundaries=bb)
 
-    got = _run(blocks, kern, IN_KERNEL, 3)
+    got = _run(blocks, kern, in_kernel, 3)
     assert torch.equal(got, _run(blocks, kern, MERGE_KERNEL, 3)), "block list splits=3"
     assert_parity(got, _oracle(q, kn, vn, cache, 700, bb), what="block list splits=3")
 
@@ -122,7 +126,7 @@ def test_in_kernel_merge_ragged_batch(device, built_lib, kernel, h):
         return ops.blockwise_causal_attention_varlen(q, k, v, kv_cache=cache, cache_lens=lens,
                                                      block_boundaries=bb)
 
-    got = _run(call, kernel[1], IN_KERNEL)
+    got = _run(call, kernel[1], kernel[2])
     assert torch.equal(got, _run(call, kernel[1], MERGE_KERNEL)), f"{kernel[0]} ragged h={h}"
     for i, c in enumerate(lens):
         assert_parity(got[i:i + 1], _oracle(q[i:i + 1], k[i:i + 1], v[i:i + 1],
@@ -149,7 +153,7 @@ def test_in_kernel_merge_repeats_and_graph_replays(device, built_lib, kernel, h)
 
     refs = [_run(lambda i=i: call(i), kernel[1], MERGE_KERNEL, 3) for i in range(3)]
     with _lib.tuning(_lib.TUNE_ATTN_KERNEL, kernel[1]), \
-            _lib.tuning(_lib.TUNE_ATTN_PMERGE, IN_KERNEL):
+            _lib.tuning(_lib.TUNE_ATTN_PMERGE, kernel[2]):
         for splits in (3, 2, 5, 3):
             with _lib.tuning(_lib.TUNE_ATTN_SPLITS, splits):
                 for i in range(3):
@@ -186,7 +190,7 @@ def test_in_kernel_merge_grouped_query(device, built_lib, kernel, heads):
         return ops.blockwise_causal_attention(q, k, v, kv_cache=cache, cache_len=c)
 
     for splits in (2, 5):
-        got = _run(call, kernel[1], IN_KERNEL, splits)
+        got = _run(call, kernel[1], kernel[2], splits)
         assert torch.equal(got, _run(call, kernel[1], MERGE_KERNEL, splits)), (
             f"{kernel[0]} GQA {h}/{hkv} splits={splits}")
         assert_parity(got, _oracle(q, k, v, cache, c), what=f"{kernel[0]} GQA {h}/{hkv}")
