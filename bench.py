@@ -61,8 +61,18 @@ def _profiled_call_us() -> dict | None:
     path = ROOT / "profiles" / "attn_fwd_C1_kernel_stats.md"
     if not path.exists():
         return None
-    m = re.search(r"profiled_us_per_call:\s*([0-9.eE+]+)", path.read_text())
-    return {"us": float(m.group(1)), "source": str(path.relative_to(ROOT))} if m else None
+    text = path.read_text()
+    m = re.search(r"profiled_us_per_call:\s*([0-9.eE+]+)", text)
+    if not m:
+        return None
+    out = {"us": float(m.group(1)), "source": str(path.relative_to(ROOT))}
+    # HIP-event time of the same call in the same profiled run: the two agree when
+    # the event method counts what the kernel trace counts.
+    e = re.search(r"event_us_same_run:\s*([0-9.eE+]+)", text)
+    if e:
+        out["event_us_same_run"] = float(e.group(1))
+        out["method_gap"] = out["event_us_same_run"] / out["us"] - 1.0
+    return out
 
 
 def _per_layer_inputs(inp, device, layers: int, cache_len: int):
