@@ -142,6 +142,52 @@ def test_matches_the_unfused_path(device, built_lib):
     assert_parity_scaled(fv, v.float(), what="v vs unfused")
 
 
+QKV_SHAPES = [(1, 83, 3072, 24, 128), (1, 128, 5120, 40, 128), (2, 16, 512, 1, 128),
+              (1, 96, 1536, 6, 64), (1, 1, 8192, 1, 128)]
+
+
+@pytest.mark.parametrize("b,l,c,heads,dim", QKV_SHAPES)
+def test_repeats_bit_for_bit(device, built_lib, b, l, c, heads, dim):
+    """Repeated calls give the same bits (the split-K partials are summed in
+    split order), and meet the bar against the oracle: 83 and 128 tokens, one
+    token over 8,192 channels, head_dim 64 and 128."""
+    args = _setup(b, l, c, heads, dim, seed=b * l + c)
+    x, ws, bs, nq, nk, cos, sin = args
+    call = lambda: ops.qkv_norm_rope(x, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], nq, nk,  # noqa: E731
+                                     cos, sin, heads)
+    first = call()
+    for _ in range(3):
+        again = call()
+        assert all(torch.equal(u, w) for u, w in zip(first, again))
+    _check(first, _oracle(*args, heads), f"{b}x{l}x{c} {heads}x{dim}")
+
+
+def test_graph_replays(device, built_lib):
+    """Captured once, replayed with eager calls in between: every replay equals
+    the eager result bit for bit."""
+    from dexter_amd.bench import harness
+    heads, dim = 24, 128
+    x, ws, bs, nq, nk, cos, sin = _setup(1, 83, 3072, heads, dim, seed=13)
+    outs = []
+
+    def step():
+        outs.clear()
+        outs.extend(ops.qkv_norm_rope(x, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], nq, nk, cos,
+                                      sin, heads))
+    step()
+    eager = [t.clone() for t in outs]
+    graph = harness.capture(step)
+    captured = list(outs)  # the graph's own output buffers
+    for _ in range(3):
+        for t in captured:
+            t.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(u, w) for u, w in zip(captured, eager))
+        step()
+        torch.cuda.synchronize()
+
+
 def test_rejects_long_chunks(device, built_lib):
     x, ws, bs, nq, nk, cos, sin = _setup(1, 129, 512, 2, 64)
     with pytest.raises(LookupError):
