@@ -470,16 +470,6 @@ __device__ __forceinline__ void dma_piece(__amdgpu_buffer_rsrc_t rsrc, const uin
                : "memory");
 }
 
-// The same, to an LDS byte address.
-__device__ __forceinline__ void dma_piece_at(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds,
-                                             uint32_t voff) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(base), "v"(voff), "s"(rsrc)
-               : "memory");
-}
-
 // Templated on the element type too, although nothing in it depends on T:
 // with one TileDma<D> shared by the bf16 and f16 kernels, hipcc (ROCm 7.2)
 // silently drops the host-side stub of whichever kernel instantiates it
@@ -2576,15 +2566,6 @@ struct DecDma {
       dma_piece_at(rv, vt + m * 1024, on[PK + m] + (dc[PK + m] & cmask) + bv);
   }
 };
-
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-  asm volatile("" ::: "memory");
-}
 
 // One half of a key tile for one compute wave: S^T = K Q^T over the tile's
 // keys [32 h, 32 h + 32), softmax, O^T += V^T P^T. Two waves of a query block

@@ -17,6 +17,33 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// One LDS DMA piece (gfx950 buffer_load_dwordx4 ... lds): 64 lanes x 16 bytes
+// from the buffer at per-lane byte offsets into LDS bytes [lds, lds + 1024),
+// lane l's 16 bytes at lds + 16 l; an offset past the descriptor's records
+// writes zeros. Inline assembly on purpose: the compiler's wait-count pass
+// treats the builtin form as an LDS write of unknown extent and puts a full
+// vmcnt wait before every later LDS read. Callers wait for their own pieces
+// explicitly (wait_vmcnt, then the barrier that publishes them). M0 holds
+// the LDS base (gfx9 LDS instructions do not read it), and the s_nop is the
+// one wait state an LDS DMA needs after M0 is written.
+__device__ __forceinline__ void dma_piece_at(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds,
+                                             uint32_t voff) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(base), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+
 // Storage types. Raw 16-bit containers so that conversions are explicit and
 // identical on every path.
 struct bf16_t { uint16_t bits; };

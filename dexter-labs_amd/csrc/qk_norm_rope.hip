@@ -581,6 +581,9 @@ static int qkv_entry(const void* x, int64_t x_sb, int64_t x_sl, int io_dtype, co
                "qkv_norm_rope: pointers must be 16-byte aligned");
   DX_CHECK_ARG(x_sb % 8 == 0 && x_sl % 8 == 0 && w_row % 8 == 0 && w_row >= C,
                "qkv_norm_rope: strides must be multiples of 8 elements (weight rows >= C)");
+  // The GEMM reads 128 weight rows through a descriptor with 32-bit offsets.
+  DX_CHECK_ARG(w_row < (int64_t(1) << 22), "qkv_norm_rope: weight row stride %lld too large",
+               (long long)w_row);
   const int64_t per16 = (tdt == DX_F32) ? 4 : 8;
   DX_CHECK_ARG(cos_sl % per16 == 0 && sin_sl % per16 == 0,
                "qkv_norm_rope: cos/sin row strides must keep rows 16-byte aligned");

@@ -4,7 +4,11 @@
 // M = 83 the product is weight-streaming bound: 57 MB of weights against
 // 0.5 MB of activations, 83 FLOP per weight byte. The kernel therefore reads
 // every weight byte once, as full 128-byte lines, from as many CUs as the
-// chip has, and keeps enough of it in flight to cover HBM latency:
+// chip has, and keeps enough of it in flight to cover HBM latency. Two forms
+// share the grid and the partial tiles: the default DMA form (qkv_dma_kernel,
+// below: two waves of 64 features, weights and activations DMA'd into LDS)
+// and the register-ring form described here (dx_set_tuning DX_TUNE_QKV_WAVES
+// 2 or 4), whose operand reads per MFMA bind it to the LDS bandwidth:
 //
 //  * Workgroup = NW waves; wave w owns 32 consecutive output features (rows of
 //    one weight), the workgroup 32 NW of them, over one K split of C / S. The
@@ -201,6 +205,162 @@ __global__ __launch_bounds__(64 * NW) void qkv_gemm_kernel(QkvGemmArgs a) {
   }
 }
 
+// LDS-lean form: two waves per workgroup, 64 output features per wave (two
+// 32-row MFMA blocks), so each activation piece read from LDS feeds two
+// MFMAs: a k-step reads 2 + NM pieces per lane for 2 NM MFMAs, where four
+// waves of 32 features read 1 + NM for NM (at the Wan-5B chunk 2.5 KB
+// instead of 4 KB of operand reads per wave per three MFMAs, below the LDS's
+// 128 bytes per clock with room for the staging writes). Weights and
+// activations land in LDS by DMA, with no register ring: per K chunk of KC the
+// workgroup's 128 weight rows and 32 NM activation rows are cut into 1 KB
+// pieces (512 / KC rows of 2 KC contiguous bytes each), and each lane fetches
+// the logical 16-byte piece that belongs at its swizzled slot. NS stages form
+// a ring: chunk c's weights and activations are issued NS - 1 chunks ahead,
+// and loads complete in order, so waiting for chunk c's pieces leaves the
+// NS - 2 younger chunks in flight. Per chunk a wave waits for its pieces of
+// chunk c, the barrier publishes them and frees the stage chunk c - 1 used,
+// the wave issues chunk c + NS - 1 into that stage and computes chunk c. Same
+// grid, splits and fp32 partial tiles as the register-ring form.
+template <int KC>
+__device__ __forceinline__ int slot_at(int r, int q) {
+  return r * 2 * KC + 16 * (q ^ (r & (KC / 8 - 1)));
+}
+
+template <typename T, int NM, int KC, int NS>
+__global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
+  constexpr int kF = 128;                            // output features per workgroup
+  constexpr int kRowB = 2 * KC;                      // bytes per row of a chunk
+  constexpr int kWBytes = kF * kRowB;                // weight part of a stage
+  constexpr int kXBytes = 32 * NM * kRowB;           // activation part of a stage
+  constexpr int kStage = kWBytes + kXBytes;
+  constexpr int kWP = kWBytes / 2048;                // weight pieces per wave per chunk
+  constexpr int kXP = kXBytes / 2048;                // activation pieces per wave per chunk
+  constexpr int kRPP = 1024 / kRowB;                 // rows per piece
+  constexpr int kQ = KC / 8;                         // 16-byte pieces per row
+  constexpr int kSteps = KC / 16;                    // MFMA k-steps per chunk
+  constexpr int kAhead = (NS - 2) * (kWP + kXP);     // pieces in flight past chunk c's
+  static_assert(kXBytes % 2048 == 0 && kWBytes % 2048 == 0, "pieces split over two waves");
+  static_assert(NS >= 2 && kAhead <= 63, "in-flight pieces fit the vmcnt counter");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
+
+  const int tid = int(threadIdx.x), lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, r = lane & 31;
+  const int split = int(blockIdx.x) % a.S, tile = int(blockIdx.x) / a.S;
+  const int n0 = tile * kF;
+  const int plane = n0 / a.HD;
+  const int k0 = split * a.Kc;
+  const int nc = a.Kc / KC;
+  const uint32_t lds0 = uint32_t(uintptr_t((__attribute__((address_space(3))) uint8_t*)lds));
+
+  // Weight rows of the tile, from column k0, through a descriptor whose base
+  // is the tile's first row (offsets stay 32-bit: 128 rows of the weight).
+  const uint16_t* wsrc = plane == 0 ? a.w[0] : plane == 1 ? a.w[1] : a.w[2];
+  const int64_t wstride = plane == 0 ? a.w_row[0] : plane == 1 ? a.w_row[1] : a.w_row[2];
+  const __amdgpu_buffer_rsrc_t wr_src = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(wsrc + int64_t(n0 - plane * a.HD) * wstride + k0), (short)0,
+      0x7ffffff0, kBufWord3);
+  // Piece i of this wave is piece 2 i + wave of the part; lane l fills slot
+  // l % kQ of its row, which holds the row's logical piece (l % kQ) ^ (row % kQ).
+  uint32_t woff[kWP];
+#pragma unroll
+  for (int i = 0; i < kWP; ++i) {
+    const int row = kRPP * (2 * i + wave) + lane / kQ;
+    const int q = (lane % kQ) ^ (row & (kQ - 1));
+    woff[i] = uint32_t(2 * (int64_t(row) * wstride + 8 * q));
+  }
+  // Activation pieces the same way; rows past M read zeros.
+  const __amdgpu_buffer_rsrc_t xr_src = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), (short)0, int(a.x_bytes), kBufWord3);
+  uint32_t xoff[kXP];
+#pragma unroll
+  for (int i = 0; i < kXP; ++i) {
+    const int row = kRPP * (2 * i + wave) + lane / kQ;
+    const int q = (lane % kQ) ^ (row & (kQ - 1));
+    const int m = min(row, a.M - 1);
+    const int b = m / a.L, l = m - b * a.L;
+    xoff[i] = row < a.M ? uint32_t(2 * (b * a.x_sb + l * a.x_sl + k0 + 8 * q)) : 0x80000000u;
+  }
+  auto issue = [&](int c) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + uint32_t((c % NS) * kStage) + 1024u * uint32_t(wave);
+    const uint32_t kb = uint32_t(2 * KC * c);
+#pragma unroll
+    for (int i = 0; i < kWP; ++i) dma_piece_at(wr_src, st + 2048u * i, woff[i] + kb);
+#pragma unroll
+    for (int i = 0; i < kXP; ++i)
+      dma_piece_at(xr_src, st + kWBytes + 2048u * i,
+                   xoff[i] >= 0x80000000u ? xoff[i] : xoff[i] + kb);
+  };
+
+  f32x16 acc[2][NM];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int t = 0; t < NM; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[b][t][e] = 0.f;
+
+#pragma unroll
+  for (int c = 0; c < NS - 1; ++c)
+    if (c < nc) issue(c);
+  for (int c = 0; c < nc; ++c) {
+    // Chunk c's pieces have landed; the NS - 2 younger chunks may still fly.
+    if (c + NS - 2 < nc) wait_vmcnt<kAhead>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (c + NS - 1 < nc) issue(c + NS - 1);
+    const uint8_t* wb = lds + (c % NS) * kStage + wave * 64 * kRowB;
+    const uint8_t* xb = lds + (c % NS) * kStage + kWBytes;
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      u32x4 wa[2], bx[NM];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        wa[b] = *reinterpret_cast<const u32x4*>(wb + slot_at<KC>(32 * b + r, kSteps * g + j));
+#pragma unroll
+      for (int t = 0; t < NM; ++t)
+        bx[t] = *reinterpret_cast<const u32x4*>(xb + slot_at<KC>(t * 32 + r, kSteps * g + j));
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int t = 0; t < NM; ++t) acc[b][t] = ProjMfma<T>::run(wa[b], bx[t], acc[b][t]);
+    }
+  }
+
+  // Partial tile: lane holds features 8 (e / 4) + 4 g + e % 4 of block b's 32,
+  // token t 32 + r.
+  const int64_t n3 = 3 * int64_t(a.HD);
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int nf = n0 + 64 * wave + 32 * b + 4 * g;
+#pragma unroll
+    for (int t = 0; t < NM; ++t) {
+      const int m = t * 32 + r;
+      if (m < a.M) {
+        float* dst = a.part + (int64_t(split) * a.M + m) * n3 + nf;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          __builtin_nontemporal_store(f32x4{acc[b][t][4 * q], acc[b][t][4 * q + 1],
+                                            acc[b][t][4 * q + 2], acc[b][t][4 * q + 3]},
+                                      reinterpret_cast<f32x4*>(dst + 8 * q));
+      }
+    }
+  }
+}
+
+// Chunk width and stages of the DMA form, measured at the Wan-5B chunk (us
+// per layer, GEMM + epilogue, 30 layers per graph): KC 64 with 3 stages
+// 21.82-21.83, 4 stages 22.00-22.06, 5 stages 22.47; KC 32 with 9 stages 25.89
+// (twice the barriers); KC 128 with 2 stages 25.21 (one chunk in flight). The
+// register-ring form (four waves of 32 features) takes 25.4-25.5.
+constexpr int kDmaKC = 64, kDmaNS = 3;
+
+template <typename T, int NM>
+hipError_t launch_dma_nm(const QkvGemmArgs& a, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((qkv_dma_kernel<T, NM, kDmaKC, kDmaNS>), dim3(blocks), dim3(128), 0, st, a);
+  return hipGetLastError();
+}
+
 template <typename T, int NW, int NM>
 hipError_t launch_nm(const QkvGemmArgs& a, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((qkv_gemm_kernel<T, NW, NM, kRing>), dim3(blocks), dim3(64 * NW), 0, st,
@@ -221,23 +381,33 @@ hipError_t launch_nw(const QkvGemmArgs& a, int blocks, hipStream_t st) {
 
 template <typename T>
 hipError_t launch_t(const QkvGemmArgs& a, const QkvPlan& p, hipStream_t st) {
+  if (p.dma) {
+    const int blocks = (3 * a.HD / 128) * a.S;
+    switch ((a.M + 31) / 32) {
+      case 1: return launch_dma_nm<T, 1>(a, blocks, st);
+      case 2: return launch_dma_nm<T, 2>(a, blocks, st);
+      case 3: return launch_dma_nm<T, 3>(a, blocks, st);
+      default: return launch_dma_nm<T, 4>(a, blocks, st);
+    }
+  }
   const int blocks = (3 * a.HD / (32 * p.waves)) * a.S;
   return p.waves == 2 ? launch_nw<T, 2>(a, blocks, st) : launch_nw<T, 4>(a, blocks, st);
 }
 
 }  // namespace
 
-// Waves per workgroup and K splits: four waves (128 output features), and the
-// split count (dividing C into whole prefetch rings of 512) whose grid comes
+// Form and K splits: the DMA form (128 output features per workgroup) unless
+// dx_set_tuning(DX_TUNE_QKV_WAVES) asks for the register-ring form with 2 or 4
+// waves; the split count (dividing C into whole rings of 512) whose grid comes
 // closest to one workgroup per CU, fewer splits on a tie. At the Wan-5B chunk
-// that is 3 splits, 216 workgroups: measured 19.9 us for the GEMM, against
-// 26.7 us at 6 splits and 22-24 us at 2 (each a read-bandwidth and
-// partial-traffic trade). dx_set_tuning(DX_TUNE_QKV_WAVES / DX_TUNE_QKV_SPLITS)
-// overrides it.
+// that is 3 splits, 216 workgroups (the register-ring GEMM measured 19.9 us
+// there, against 26.7 us at 6 splits and 22-24 us at 2: each a read-bandwidth
+// and partial-traffic trade). DX_TUNE_QKV_SPLITS overrides the split count.
 QkvPlan plan_qkv(int64_t M, int64_t C, int64_t HD) {
   QkvPlan p{};
-  p.waves = 4;
-  if (tuning(DX_TUNE_QKV_WAVES) == 2) p.waves = 2;
+  const long waves = tuning(DX_TUNE_QKV_WAVES);
+  p.dma = waves != 2 && waves != 4;
+  p.waves = waves == 2 ? 2 : 4;
   const int64_t tiles = 3 * HD / (32 * p.waves);
   int s = 1;
   int64_t best = -1;

@@ -188,6 +188,21 @@ def test_graph_replays(device, built_lib):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("waves", [2, 4])
+def test_register_ring_form_under_tuning(device, built_lib, waves):
+    """dx_set_tuning(DX_TUNE_QKV_WAVES, 2 or 4) selects the register-ring GEMM
+    (weights through registers into per-wave LDS chunks) instead of the DMA
+    form: it meets the same bar, at 83 and 128 tokens."""
+    from dexter_amd.ops.gfx950 import _lib
+    for shape in [(1, 83, 3072, 24, 128), (4, 32, 3072, 48, 64)]:
+        args = _setup(*shape, seed=shape[1] + waves)
+        x, ws, bs, nq, nk, cos, sin = args
+        with _lib.tuning(_lib.TUNE_QKV_WAVES, waves):
+            got = ops.qkv_norm_rope(x, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], nq, nk, cos,
+                                    sin, shape[3])
+        _check(got, _oracle(*args, shape[3]), f"ring{waves} {shape}")
+
+
 def test_rejects_long_chunks(device, built_lib):
     x, ws, bs, nq, nk, cos, sin = _setup(1, 129, 512, 2, 64)
     with pytest.raises(LookupError):
