@@ -17,7 +17,7 @@ struct QkvGemmArgs {
 
 // Plan of one projection launch on the current device.
 struct QkvPlan {
-  bool dma;    // the LDS-lean DMA form (two waves of 64 features, 128 per workgroup)
+  bool dma;    // the LDS-lean DMA form (waves of 64 features, 128 per workgroup)
   int waves;   // register-ring form: waves per workgroup = 32-row output subtiles
   int splits;  // K splits (partials)
   int64_t workspace_bytes;

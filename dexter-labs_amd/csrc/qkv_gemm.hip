@@ -6,7 +6,7 @@
 // every weight byte once, as full 128-byte lines, from as many CUs as the
 // chip has, and keeps enough of it in flight to cover HBM latency. Two forms
 // share the grid and the partial tiles: the default DMA form (qkv_dma_kernel,
-// below: two waves of 64 features, weights and activations DMA'd into LDS)
+// below: waves of 64 features, weights and activations DMA'd into LDS)
 // and the register-ring form described here (dx_set_tuning DX_TUNE_QKV_WAVES
 // 2 or 4), whose operand reads per MFMA bind it to the LDS bandwidth:
 //
@@ -205,12 +205,14 @@ __global__ __launch_bounds__(64 * NW) void qkv_gemm_kernel(QkvGemmArgs a) {
   }
 }
 
-// LDS-lean form: two waves per workgroup, 64 output features per wave (two
-// 32-row MFMA blocks), so each activation piece read from LDS feeds two
-// MFMAs: a k-step reads 2 + NM pieces per lane for 2 NM MFMAs, where four
-// waves of 32 features read 1 + NM for NM (at the Wan-5B chunk 2.5 KB
-// instead of 4 KB of operand reads per wave per three MFMAs, below the LDS's
-// 128 bytes per clock with room for the staging writes). Weights and
+// LDS-lean form: 64 output features per wave (two 32-row MFMA blocks), so
+// each activation piece read from LDS feeds two MFMAs: a k-step reads 2 + NM
+// pieces per lane for 2 NM MFMAs, where waves of 32 features read 1 + NM for
+// NM (at the Wan-5B chunk 2.5 KB instead of 4 KB of operand reads per three
+// MFMAs, below the LDS's 128 bytes per clock with room for the staging
+// writes). Two waves cover the workgroup's 128 features; with NWV = 4 a second
+// pair takes the other half of every chunk's k-steps, and the pairs' sums are
+// added through LDS before the store. Weights and
 // activations land in LDS by DMA, with no register ring: per K chunk of KC the
 // workgroup's 128 weight rows and 32 NM activation rows are cut into 1 KB
 // pieces (512 / KC rows of 2 KC contiguous bytes each), and each lane fetches
@@ -226,25 +228,31 @@ __device__ __forceinline__ int slot_at(int r, int q) {
   return r * 2 * KC + 16 * (q ^ (r & (KC / 8 - 1)));
 }
 
-template <typename T, int NM, int KC, int NS>
-__global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
+template <typename T, int NM, int KC, int NS, int NWV>
+__global__ __launch_bounds__(64 * NWV) void qkv_dma_kernel(QkvGemmArgs a) {
   constexpr int kF = 128;                            // output features per workgroup
+  constexpr int kKH = NWV / 2;                       // waves sharing a feature half (K halves)
   constexpr int kRowB = 2 * KC;                      // bytes per row of a chunk
   constexpr int kWBytes = kF * kRowB;                // weight part of a stage
   constexpr int kXBytes = 32 * NM * kRowB;           // activation part of a stage
   constexpr int kStage = kWBytes + kXBytes;
-  constexpr int kWP = kWBytes / 2048;                // weight pieces per wave per chunk
-  constexpr int kXP = kXBytes / 2048;                // activation pieces per wave per chunk
+  constexpr int kWP = kWBytes / (1024 * NWV);        // weight pieces per wave per chunk
+  constexpr int kXP = kXBytes / (1024 * NWV);        // activation pieces per wave per chunk
   constexpr int kRPP = 1024 / kRowB;                 // rows per piece
   constexpr int kQ = KC / 8;                         // 16-byte pieces per row
   constexpr int kSteps = KC / 16;                    // MFMA k-steps per chunk
   constexpr int kAhead = (NS - 2) * (kWP + kXP);     // pieces in flight past chunk c's
-  static_assert(kXBytes % 2048 == 0 && kWBytes % 2048 == 0, "pieces split over two waves");
+  static_assert(NWV == 2 || NWV == 4, "two waves, or two per feature half");
+  static_assert(kXBytes % (1024 * NWV) == 0 && kWBytes % (1024 * NWV) == 0,
+                "pieces split evenly over the waves");
+  static_assert(kSteps % kKH == 0, "k-steps split evenly over the K halves");
   static_assert(NS >= 2 && kAhead <= 63, "in-flight pieces fit the vmcnt counter");
+  static_assert(kKH == 1 || 2 * 64 * 2 * NM * 16 * 4 <= NS * kStage, "exchange fits the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
 
   const int tid = int(threadIdx.x), lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fw = wave & 1, kh = wave >> 1;  // feature half, K half of each chunk
   const int g = lane >> 5, r = lane & 31;
   const int split = int(blockIdx.x) % a.S, tile = int(blockIdx.x) / a.S;
   const int n0 = tile * kF;
@@ -260,12 +268,12 @@ __global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
   const __amdgpu_buffer_rsrc_t wr_src = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(wsrc + int64_t(n0 - plane * a.HD) * wstride + k0), (short)0,
       0x7ffffff0, kBufWord3);
-  // Piece i of this wave is piece 2 i + wave of the part; lane l fills slot
+  // Piece i of this wave is piece NWV i + wave of the part; lane l fills slot
   // l % kQ of its row, which holds the row's logical piece (l % kQ) ^ (row % kQ).
   uint32_t woff[kWP];
 #pragma unroll
   for (int i = 0; i < kWP; ++i) {
-    const int row = kRPP * (2 * i + wave) + lane / kQ;
+    const int row = kRPP * (NWV * i + wave) + lane / kQ;
     const int q = (lane % kQ) ^ (row & (kQ - 1));
     woff[i] = uint32_t(2 * (int64_t(row) * wstride + 8 * q));
   }
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
   uint32_t xoff[kXP];
 #pragma unroll
   for (int i = 0; i < kXP; ++i) {
-    const int row = kRPP * (2 * i + wave) + lane / kQ;
+    const int row = kRPP * (NWV * i + wave) + lane / kQ;
     const int q = (lane % kQ) ^ (row & (kQ - 1));
     const int m = min(row, a.M - 1);
     const int b = m / a.L, l = m - b * a.L;
@@ -285,10 +293,10 @@ __global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
     const uint32_t st = lds0 + uint32_t((c % NS) * kStage) + 1024u * uint32_t(wave);
     const uint32_t kb = uint32_t(2 * KC * c);
 #pragma unroll
-    for (int i = 0; i < kWP; ++i) dma_piece_at(wr_src, st + 2048u * i, woff[i] + kb);
+    for (int i = 0; i < kWP; ++i) dma_piece_at(wr_src, st + 1024u * NWV * i, woff[i] + kb);
 #pragma unroll
     for (int i = 0; i < kXP; ++i)
-      dma_piece_at(xr_src, st + kWBytes + 2048u * i,
+      dma_piece_at(xr_src, st + kWBytes + 1024u * NWV * i,
                    xoff[i] >= 0x80000000u ? xoff[i] : xoff[i] + kb);
   };
 
@@ -309,10 +317,11 @@ __global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
     else wait_vmcnt<0>();
     __syncthreads();
     if (c + NS - 1 < nc) issue(c + NS - 1);
-    const uint8_t* wb = lds + (c % NS) * kStage + wave * 64 * kRowB;
+    const uint8_t* wb = lds + (c % NS) * kStage + fw * 64 * kRowB;
     const uint8_t* xb = lds + (c % NS) * kStage + kWBytes;
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
+    for (int jj = 0; jj < kSteps / kKH; ++jj) {
+      const int j = kh * (kSteps / kKH) + jj;
       u32x4 wa[2], bx[NM];
 #pragma unroll
       for (int b = 0; b < 2; ++b)
@@ -327,12 +336,42 @@ __global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
     }
   }
 
+  if (kKH == 2) {
+    // The second K half's sums join the first's through the (now idle) ring:
+    // f32x4 (fw, b, t, q) of every lane, consecutive lanes adjacent.
+    f32x4* ex = reinterpret_cast<f32x4*>(lds);
+    __syncthreads();
+    if (kh == 1) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int t = 0; t < NM; ++t)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            ex[(((fw * 2 + b) * NM + t) * 4 + q) * 64 + lane] =
+                f32x4{acc[b][t][4 * q], acc[b][t][4 * q + 1], acc[b][t][4 * q + 2],
+                      acc[b][t][4 * q + 3]};
+    }
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int t = 0; t < NM; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 o = ex[(((fw * 2 + b) * NM + t) * 4 + q) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[b][t][4 * q + e] += o[e];
+        }
+  }
+
   // Partial tile: lane holds features 8 (e / 4) + 4 g + e % 4 of block b's 32,
   // token t 32 + r.
   const int64_t n3 = 3 * int64_t(a.HD);
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    const int nf = n0 + 64 * wave + 32 * b + 4 * g;
+    const int nf = n0 + 64 * fw + 32 * b + 4 * g;
 #pragma unroll
     for (int t = 0; t < NM; ++t) {
       const int m = t * 32 + r;
@@ -348,16 +387,20 @@ __global__ __launch_bounds__(128) void qkv_dma_kernel(QkvGemmArgs a) {
   }
 }
 
-// Chunk width and stages of the DMA form, measured at the Wan-5B chunk (us
-// per layer, GEMM + epilogue, 30 layers per graph): KC 64 with 3 stages
-// 21.82-21.83, 4 stages 22.00-22.06, 5 stages 22.47; KC 32 with 9 stages 25.89
-// (twice the barriers); KC 128 with 2 stages 25.21 (one chunk in flight). The
-// register-ring form (four waves of 32 features) takes 25.4-25.5.
-constexpr int kDmaKC = 64, kDmaNS = 3;
+// Chunk width, stages and waves of the DMA form, measured at the Wan-5B chunk
+// (us per layer, GEMM + epilogue, 30 layers per graph). Two waves: KC 64 with
+// 3 stages 21.82-21.83, 4 stages 22.00-22.06, 5 stages 22.47; KC 32 with 9
+// stages 25.89 (twice the barriers); KC 128 with 2 stages 25.21 (one chunk in
+// flight). Four waves (each feature half's k-steps split over two waves, so
+// the MFMAs use all four SIMDs; the halves' sums meet through LDS at the end):
+// KC 64 with 3 stages 21.47-21.55, 4 stages 21.43, KC 128 with 2 stages 24.76.
+// The register-ring form (four waves of 32 features) takes 25.4-25.5.
+constexpr int kDmaKC = 64, kDmaNS = 3, kDmaWaves = 4;
 
 template <typename T, int NM>
 hipError_t launch_dma_nm(const QkvGemmArgs& a, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((qkv_dma_kernel<T, NM, kDmaKC, kDmaNS>), dim3(blocks), dim3(128), 0, st, a);
+  hipLaunchKernelGGL((qkv_dma_kernel<T, NM, kDmaKC, kDmaNS, kDmaWaves>), dim3(blocks),
+                     dim3(64 * kDmaWaves), 0, st, a);
   return hipGetLastError();
 }
 

@@ -89,8 +89,8 @@ int dx_abi_version(void);
  *                        4 one-launch decode
  *   DX_TUNE_NORM_WAVES   waves per row of the adaLN / gated-residual kernels (1..16)
  *   DX_TUNE_QKV_SPLITS   K splits of the fused QKV GEMM (1..16)
- *   DX_TUNE_QKV_WAVES    fused QKV GEMM form: 0 the LDS-DMA form (two waves of
- *                        64 features), 2 or 4 the register-ring form with that
+ *   DX_TUNE_QKV_WAVES    fused QKV GEMM form: 0 the LDS-DMA form (waves of 64
+ *                        features), 2 or 4 the register-ring form with that
  *                        many waves of 32 features
  *   DX_TUNE_ATTN_MERGE   one-launch decode merge: 1 through the L2 when the
  *                        splits share an XCD (the default), 2 at device
