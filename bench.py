@@ -72,6 +72,11 @@ def _profiled_call_us() -> dict | None:
     if e:
         out["event_us_same_run"] = float(e.group(1))
         out["method_gap"] = out["event_us_same_run"] / out["us"] - 1.0
+    # The same command without the profiler, as committed: the figure this line's
+    # live launch_us is checked against.
+    u = re.search(r"unprofiled_us_per_call:\s*([0-9.eE+]+)", text)
+    if u:
+        out["unprofiled_us_committed"] = float(u.group(1))
     return out
 
 
@@ -190,6 +195,8 @@ def run_headline(args, device):
         # lengthened by the profiler's instrumentation): the frac the committed
         # profile gives, beside the live HIP-event one.
         profiled["frac"] = attn_bytes / (profiled["us"] * 1e-6) / 1e9 / PEAK_HBM_GBPS
+        if "unprofiled_us_committed" in profiled:
+            profiled["live_vs_committed"] = attn_ms * 1e3 / profiled["unprofiled_us_committed"] - 1.0
     return {
         "ms_per_step": ms_per_step,
         "value": value,
