@@ -1622,10 +1622,11 @@ __device__ __forceinline__ void spread_split_group(const AttnArgs& a, const Coor
 // head_dim blocks [s DT / 2, (s + 1) DT / 2) of its wave's 32 rows (r0 ..)
 // and the whole row's (l_tot, mref). Both streams pack their blocks into the
 // row area at ``area``; after a workgroup barrier each stores 16 of the 32
-// rows, whole. A split partial takes one scale exponent per row
-// (partial_scale), from the row's largest |value| over both streams' blocks,
-// exchanged through ``ax`` (2 x 64 kNW floats of idle LDS). Every wave of the
-// workgroup calls it (the barriers); ``active``: the wave has rows below Lq.
+// rows, whole. A split partial takes one scale exponent per row (as
+// partial_scale's), from ``rbound``: an upper bound of the row's largest
+// |value| over both streams' blocks that the hand-over already carried, so no
+// exchange of the combined maxima is needed. Every wave of the workgroup
+// calls it (the barrier); ``active``: the wave has rows below Lq.
 // The stream is a template parameter so that every block index is a constant
 // (a register array indexed at run time would live in scratch memory).
 template <int D, typename T, int stream, int kAux = 0>
@@ -1633,10 +1634,10 @@ __device__ __forceinline__ int store_result_halves(const AttnArgs& a, const Coor
                                                     int r0, int g, int lane, int ltid,
                                                     bool active,
                                                     const f32x16 (&acc)[D / 32], float l_tot,
-                                                    float mref, uint32_t area, float* ax) {
+                                                    float mref, uint32_t area, float rbound) {
   // As in store_result_staged: each product rounded to fp32, then converted.
 #pragma clang fp contract(off)
-  constexpr int DT = D / 32, HB = DT / 2, LANES = 64 * kNW;
+  constexpr int DT = D / 32, HB = DT / 2;
   constexpr int d0 = stream * HB;
   using A = RowArea<D>;
   const int row = r0 + (lane & 31);
@@ -1646,17 +1647,8 @@ __device__ __forceinline__ int store_result_halves(const AttnArgs& a, const Coor
   if (it.n_splits == 1) {
     k = 1.0f / l_tot;
   } else {
-    float amax = 0.f;
-#pragma unroll
-    for (int dd = 0; dd < HB; ++dd)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(acc[d0 + dd][r]));
-    amax = xor32_max(amax);  // the row's other half of each block (lanes l and l ^ 32)
-    ax[stream * LANES + ltid] = amax;
-    __syncthreads();
-    amax = fmaxf(amax, ax[(1 - stream) * LANES + ltid]);  // the other stream's blocks
     const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-    const float omax = amax * inv;
+    const float omax = rbound * inv;
     e = omax > 0.f && omax <= FLT_MAX ? __builtin_amdgcn_frexp_expf(omax) : 0;
     k = __builtin_ldexpf(inv, -e);
   }
@@ -1953,8 +1945,8 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
     auto epilogue = [&](auto stream_c) __attribute__((always_inline)) {
       constexpr int S = decltype(stream_c)::value;
       constexpr int LANES = 64 * kNW, HB = DT / 2, NV = 1 + 4 * HB;
-      static_assert(2 * NV * LANES * 16 + 2 * LANES * 4 <= Lds<D>::bytes,
-                    "the hand-over and the max exchange lie below the row area");
+      static_assert(2 * NV * LANES * 16 <= Lds<D>::bytes,
+                    "the hand-over lies below the row area");
       f32x4* const x = reinterpret_cast<f32x4*>(smem);
       f32x4* const hand = x + S * NV * LANES;
       const f32x4* const got = x + (1 - S) * NV * LANES;
@@ -1968,7 +1960,16 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
         DX_NOTE(10, xcc);
       }
 #endif
-      hand[ltid] = f32x4{mref, sm.l, 0.f, 0.f};
+      // This stream's largest |acc| in each row, over all head_dim blocks: with
+      // the other stream's, weighted as the combine weights them, it bounds
+      // the combined row's largest |value| (a split partial's scale exponent).
+      float amax = 0.f;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) amax = fmaxf(amax, fabsf(acc[d][r]));
+      amax = xor32_max(amax);  // the row's other half of each block (lanes l and l ^ 32)
+      hand[ltid] = f32x4{mref, sm.l, amax, 0.f};
 #pragma unroll
       for (int dd = 0; dd < HB; ++dd)
 #pragma unroll
@@ -1988,6 +1989,8 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       const float w0 = fast_exp2(m0 - base), w1 = fast_exp2(m1 - base);
       // One explicit rounding order, so that both streams hold the same l.
       sm.l = __builtin_fmaf(l0, w0, l1 * w1);
+      const float x0 = s0 ? amax : h[2], x1 = s0 ? h[2] : amax;
+      const float rbound = __builtin_fmaf(x0, w0, x1 * w1);
 #pragma unroll
       for (int dd = 0; dd < HB; ++dd)
 #pragma unroll
@@ -2005,10 +2008,9 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       const float l_tot = xor32_sum(sm.l);
       // Result rows through stream 1's tile buffers, past the hand-over area.
       const uint32_t area = lds_addr(smem) + Lds<D>::bytes;
-      float* const ax = reinterpret_cast<float*>(x + 2 * NV * LANES);
       if (!merge_here) {
         store_result_halves<D, T, S>(a, it, q0, wave * 32, g, lane, ltid, wave_active, acc,
-                                     l_tot, mref, area, ax);
+                                     l_tot, mref, area, rbound);
         DX_STAMP(4);
         DX_NOTE(8, uint32_t(it.split) | uint32_t(it.n_splits) << 8 | uint32_t(it.b) << 16);
         DX_STAMP(7);
@@ -2021,7 +2023,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
         // (spread_split_group): the partial goes to this XCD's L2; every
         // split then merges its chunk of rows once the group has arrived.
         const int e = store_result_halves<D, T, S>(a, it, q0, wave * 32, g, lane, ltid,
-                                                   wave_active, acc, l_tot, mref, area, ax);
+                                                   wave_active, acc, l_tot, mref, area, rbound);
         DX_STAMP(4);
         spread_split_group<D, T, kBM, 64 * kNW * NS>(
             a, it, q0, smem, [&]() __attribute__((always_inline)) {
@@ -2033,7 +2035,7 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       // Split, merged in this launch: store the partial, then every wave
       // arrives (arrive_split_group); the last split of the group merges.
       store_result_halves<D, T, S, kScDevice>(a, it, q0, wave * 32, g, lane, ltid, wave_active,
-                                              acc, l_tot, mref, area, ax);
+                                              acc, l_tot, mref, area, rbound);
       DX_STAMP(4);
       arrive_split_group<D, T, kBM, 64 * kNW * NS, 2>(a, it, q0, smem);
     };
