@@ -364,7 +364,7 @@ int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t 
  * (row stride w_row, the nn.Linear weight layout); bq/bk/bv are [H*D] or NULL.
  * q_out, k_out, v_out are contiguous [B, L, H, D]. Limits: B*L <= 128 tokens
  * (decode chunks), C a multiple of 512, H*D a multiple of 128 and at most
- * 8192, x spanning less than 2^31 bytes. workspace: dx_qkv_workspace_bytes(...) bytes, 16-byte aligned (fp32
+ * 8192, x spanning less than 2^31 bytes, w_row below 2^22 elements. workspace: dx_qkv_workspace_bytes(...) bytes, 16-byte aligned (fp32
  * split-K partial products; no initialisation needed).
  * Replaces: models/dreamzero/model.py:162-175 (three nn.Linear, then
  * ops.qk_norm_rope and KVCache.append).
