@@ -53,7 +53,7 @@
 // on one XCD (item i runs on XCD i % 8), so its K/V and partials stay in one
 // L2. Ragged batches (one cache length per sequence) get one segment per
 // sequence with its own split count, longest sequence first.
-#include "dx_common.h"
+#include "attn_common.h"
 
 #include <float.h>
 #include <limits.h>
@@ -104,70 +104,8 @@ __device__ __forceinline__ void timeline_merge_word(int k) {
 constexpr int kBN = 64;        // keys per tile
 constexpr int kNW = 4;         // waves per workgroup
 constexpr int kBM = 32 * kNW;  // queries per workgroup
-constexpr int kMaxSeg = 64;    // sequences with their own cache length
-constexpr int kMaxSplits = 16;
 constexpr int kPairWaves = 8;  // waves per workgroup of the paired-group kernel
 constexpr int kBMPair = 256;   // its queries per workgroup
-
-struct AttnArgs {
-  const uint16_t* q; int64_t q_sb, q_sl, q_sh;
-  const uint16_t* k; int64_t k_sb, k_sl, k_sh;
-  const uint16_t* v; int64_t v_sb, v_sl, v_sh;
-  const uint16_t* ck; const uint16_t* cv; int64_t c_sb, c_ss, c_sh;
-  uint16_t* out; int64_t o_sb, o_sl, o_sh;
-  uint16_t* ws_o;  // [partials][bm][D] f16 partial outputs acc / l scaled by 2^-e
-  float* ws_ml;    // [partials][bm][4] {exponent reference m (log2 units), sum l, scale exponent e, 0}
-  const void* starts; int starts_i64; int n_blocks;
-  int B, H, Lq, Lk;
-  int kv_group;      // query heads per K/V head (grouped-query attention; 1 = one each)
-  int causal;
-  int n_qtiles;
-  int bm;            // queries per work item: 128 (dual-stream decode) or 256 (paired groups)
-  int comb_chunks;   // merge-kernel blocks per work-item group (rows min(bm, Lq) only)
-  float scale_log2;  // |softmax scale| * log2(e)
-  int negate_q;      // softmax scale < 0: q enters negated (exact), scale as |scale|
-  int cache_len;     // uniform mode
-  int n_splits;      // uniform mode
-  // Segment table (ragged batches): segment i covers sequence seg_b[i] with
-  // seg_splits[i] splits, work items [seg_base[i], seg_base[i+1]) and combine
-  // blocks [comb_base[i], comb_base[i+1]). n_seg == 0: one uniform segment
-  // over all B*H (batch, head) pairs.
-  int n_seg;
-  // Device-resident cache length (uniform mode): when set, the kernels read
-  // the cached row count from this int32 at launch, clamped to [0, cache_len]
-  // (cache_len then holds the cache capacity the launch was planned for), so
-  // a captured graph follows the cache as it grows between replays.
-  const int32_t* cache_len_dev;
-  // Single-launch decode: the merge state of each work-item group
-  // (kCounterStride ints, indexed by the group's first partial), zero before
-  // the launch and returned to zero by the group's workgroups.
-  int32_t* counters;
-  // Time a workgroup waits for its group on the L2 fast path of the
-  // in-kernel merge (s_memrealtime ticks); 0 skips the fast path.
-  uint32_t fast_ticks;
-  // Dual-stream kernel, split groups merged in the launch: spread the merge
-  // over the group's splits (spread_split_group) instead of leaving it to
-  // the last one to arrive (arrive_split_group).
-  int spread;
-  int seg_b[kMaxSeg], seg_splits[kMaxSeg], seg_cache[kMaxSeg];
-  int seg_base[kMaxSeg + 1], comb_base[kMaxSeg + 1];
-};
-
-// Touch every 64-byte line of the argument header up front: four
-// independent scalar loads and one wait, instead of the chain of dependent
-// loads (each a cache miss at kernel start) that the first uses would
-// otherwise issue one after another.
-__device__ __forceinline__ void prefetch_args(const AttnArgs& a) {
-  static_assert(offsetof(AttnArgs, n_seg) < 256, "argument header spans four lines");
-  static_assert(offsetof(AttnArgs, cache_len_dev) / 64 == 4 && offsetof(AttnArgs, counters) / 64 == 4,
-                "device cache length and counters on line five");
-  const uint64_t l0 = reinterpret_cast<uint64_t>(a.q);
-  const uint64_t l1 = uint64_t(a.v_sb);
-  const uint64_t l2 = uint64_t(a.c_sh);
-  const uint32_t l3 = uint32_t(a.n_seg);
-  const uint64_t l4 = reinterpret_cast<uint64_t>(a.cache_len_dev);
-  asm volatile("" ::"s"(l0), "s"(l1), "s"(l2), "s"(l3), "s"(l4));
-}
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16_t> {
@@ -206,97 +144,6 @@ template <> struct Mfma<f16_t> {
 };
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Block start i, read through the constant address space: the list does not
-// change while a kernel runs, and that lets the compiler use scalar loads
-// (counted by lgkmcnt) instead of vector loads, whose waits would also wait
-// for every tile load in flight.
-typedef __attribute__((address_space(4))) const int32_t const_i32;
-typedef __attribute__((address_space(4))) const int64_t const_i64;
-__device__ __forceinline__ int load_start(const AttnArgs& a, int i) {
-  // A generic pointer to device memory is its global address: convert it
-  // through the integer value.
-  const uint64_t p = reinterpret_cast<uint64_t>(a.starts);
-  return a.starts_i64 ? int(((const_i64*)p)[i]) : ((const_i32*)p)[i];
-}
-
-// Python's slice bound: index x of a length-n axis, negatives counted from the end.
-__device__ __forceinline__ int slice_at(int x, int n) { return x < 0 ? max(x + n, 0) : min(x, n); }
-
-// The block list as the reference reads it: pairs (lo, hi) of consecutive
-// entries of (starts..., Lq), each setting mask[lo:hi, :hi] (rows by Python
-// slicing, current keys [0, min(hi, Lq))). The starts are read 16 (+1) at a
-// time as independent scalar loads, so each batch is one memory round trip
-// instead of a chain of dependent ones; fn(lo, hi) sees every pair in order.
-template <typename Fn>
-__device__ __forceinline__ void for_each_block(const AttnArgs& a, Fn&& fn) {
-  const int nb = a.n_blocks;
-  for (int base = 0; base < nb; base += 16) {
-    int st[17];
-#pragma unroll
-    for (int u = 0; u < 17; ++u) st[u] = base + u < nb ? load_start(a, base + u) : a.Lq;
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      if (base + u < nb) fn(st[u], st[u + 1]);
-  }
-}
-
-// Current keys [0, e) that the pair's column slice [cache_len : cache_len + hi]
-// of the reference's [Lq, cache_len + Lq] mask sets, by Python's slice rules:
-// min(hi, Lq) for hi >= 0; for a negative hi, nothing while the stop
-// cache_len + hi is still >= 0 (it lies before the slice's start), and once it
-// is negative it counts from the end of the key axis, leaving the current keys
-// [0, cache_len + Lq + hi) (at least none).
-__device__ __forceinline__ int pair_end(int hi, int cache_len, int Lq) {
-  if (hi >= 0) return min(hi, Lq);
-  return cache_len + hi < 0 ? max(cache_len + Lq + hi, 0) : 0;
-}
-
-// End (exclusive, in current-key coordinates) of the keys query i may see:
-// the union of the block pairs whose row slice holds i, i.e. the largest
-// pair_end among them, 0 when no pair holds i (such a row sees only the
-// cache). For ascending starts this is the end of i's own block, and rows
-// before the first start see no current key.
-__device__ __forceinline__ int visible_end(const AttnArgs& a, int i, int cache_len) {
-  if (a.causal) return i + 1;
-  if (a.n_blocks == 0) return a.Lk;
-  int e = 0;
-  for_each_block(a, [&](int lo, int hi) __attribute__((always_inline)) {
-    if (i >= slice_at(lo, a.Lq) && i < slice_at(hi, a.Lq)) e = max(e, pair_end(hi, cache_len, a.Lq));
-  });
-  return e;
-}
-
-// Visible-end bounds (current-key coordinates) over the rows [q_first,
-// q_last] of a work item: lo <= visible_end(i) <= hi for each of them.
-// Workgroup-uniform scalar work. With causal, no blocks, or block starts that
-// are ascending and non-negative, visible_end is non-decreasing in i and the
-// end rows give exact bounds. Any other list (the reference accepts one) gets
-// the widest bounds, [0, Lq]: every current tile is visited and masked per
-// key, so results stay exact and only the whole-tile skipping is lost.
-struct EndBounds { int lo, hi; };
-__device__ __forceinline__ EndBounds end_bounds(const AttnArgs& a, int q_first, int q_last) {
-  if (a.causal || a.n_blocks == 0)
-    return {__builtin_amdgcn_readfirstlane(visible_end(a, q_first, 0)),
-            __builtin_amdgcn_readfirstlane(visible_end(a, q_last, 0))};
-  bool ascending = true;
-  int prev = 0;
-  int e_first = 0, e_last = 0;
-  for_each_block(a, [&](int lo, int hi) __attribute__((always_inline)) {
-    ascending = ascending && lo >= prev;
-    prev = lo;
-    if (q_first >= slice_at(lo, a.Lq) && q_first < slice_at(hi, a.Lq))
-      e_first = max(e_first, min(hi, a.Lq));
-    if (q_last >= slice_at(lo, a.Lq) && q_last < slice_at(hi, a.Lq))
-      e_last = max(e_last, min(hi, a.Lq));
-  });
-  // Uniform by construction (kernel arguments and workgroup-uniform rows);
-  // readfirstlane lets the compiler keep the buffer descriptors built from
-  // these bounds in scalar registers.
-  return ascending ? EndBounds{__builtin_amdgcn_readfirstlane(e_first),
-                               __builtin_amdgcn_readfirstlane(e_last)}
-                   : EndBounds{0, a.Lq};
-}
 
 // LDS geometry, per stage: a K tile [64 keys][D] and a V tile [64 keys][D],
 // both row-major as they lie in memory.
@@ -1242,13 +1089,6 @@ __device__ __forceinline__ void store_result_staged(const AttnArgs& a, const Coo
   A::template store_rows<kAux>(ro, ro_bytes, nrows, area, r0, lane);
 }
 
-// Merge state of each work-item group (arrival and finish counters, chunk
-// claims), indexed by the group's first partial, in a region of fixed size at
-// the start of every attention workspace, so that no plan's partials ever
-// overlap another plan's state. Zero before a launch, zero after it.
-constexpr int kCounterStride = 16;           // ints per group state (arrivals, finished, claims)
-constexpr int kCounterSlots = 4096;          // partials a launch that merges in-kernel may have
-constexpr int64_t kCounterRegion = int64_t(kCounterSlots) * kCounterStride * 4;  // 256 KB
 // Key splits of a work-item group merged in the kernel itself (paired and
 // dual-stream kernels), with no merge launch: every split stores its partial
 // at device scope (kScDevice), waits until the stores have completed and
@@ -3636,10 +3476,14 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
                     const void* starts, int starts_dtype, int64_t n_blocks, int causal,
                     float softmax_scale, void* workspace, int64_t ws_bytes, void* stream,
                     bool from_scratch = false) {
-  DX_CHECK_ARG(dtype == DX_BF16 || dtype == DX_F16,
-               "attention: dtype code %d unsupported (bf16 or f16)", dtype);
-  DX_CHECK_ARG(D == 64 || D == 128, "attention: head_dim %lld unsupported (64 or 128)",
+  DX_CHECK_ARG(dtype == DX_BF16 || dtype == DX_F16 || dtype == DX_F32,
+               "attention: dtype code %d unsupported (bf16, f16 or f32)", dtype);
+  DX_CHECK_ARG(any_head_dim(D), "attention: head_dim %lld unsupported (16, 32, 64, 128 or 256)",
                (long long)D);
+  // bf16/f16 at head dim 64 or 128 take the MFMA kernels of this file; fp32
+  // and the other head dims take the general kernel (attn_any.hip).
+  const bool general = dtype == DX_F32 || (D != 64 && D != 128);
+  const int64_t es = dtype == DX_F32 ? 4 : 2;
   DX_CHECK_ARG(B >= 0 && Lq >= 0 && Lk >= 0 && H > 0, "attention: bad shape");
   DX_CHECK_ARG(Hkv > 0 && H % Hkv == 0,
                "attention: %lld query heads are not a multiple of %lld k/v heads", (long long)H,
@@ -3672,41 +3516,98 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   DX_CHECK_ARG(q && k && v && out, "attention: null pointer");
   DX_CHECK_ARG(al16(q) && al16(k) && al16(v) && al16(out) && (!cache || al16(cache)),
                "attention: pointers must be 16-byte aligned");
-  DX_CHECK_ARG(q_sb % 8 == 0 && q_sl % 8 == 0 && q_sh % 8 == 0 && k_sb % 8 == 0 &&
-                   k_sl % 8 == 0 && k_sh % 8 == 0 && v_sb % 8 == 0 && v_sl % 8 == 0 &&
-                   v_sh % 8 == 0 && o_sb % 8 == 0 && o_sl % 8 == 0 && o_sh % 8 == 0 &&
-                   (!cache || (c_plane % 8 == 0 && c_sb % 8 == 0 && c_ss % 8 == 0 &&
-                               c_sh % 8 == 0)),
-               "attention: strides must be multiples of 8 elements");
+  {
+    // Rows start 16-byte aligned: every stride a multiple of 16 bytes.
+    const int64_t per16 = 16 / es;
+    DX_CHECK_ARG(q_sb % per16 == 0 && q_sl % per16 == 0 && q_sh % per16 == 0 &&
+                     k_sb % per16 == 0 && k_sl % per16 == 0 && k_sh % per16 == 0 &&
+                     v_sb % per16 == 0 && v_sl % per16 == 0 && v_sh % per16 == 0 &&
+                     o_sb % per16 == 0 && o_sl % per16 == 0 && o_sh % per16 == 0 &&
+                     (!cache || (c_plane % per16 == 0 && c_sb % per16 == 0 &&
+                                 c_ss % per16 == 0 && c_sh % per16 == 0)),
+                 "attention: strides must be multiples of %lld elements (16 bytes)",
+                 (long long)per16);
+  }
   {
     // Key/value rows are addressed with 32-bit byte offsets per (batch, head).
     const int64_t rows = max_cache + Lk;
     const int64_t stride = std::max({cache ? c_ss : int64_t(0), k_sl, v_sl});
-    DX_CHECK_ARG(rows * stride * 2 < (int64_t(1) << 31),
+    DX_CHECK_ARG(rows * stride * es < (int64_t(1) << 31),
                  "attention: %lld rows of stride %lld exceed 32-bit offsets", (long long)rows,
                  (long long)stride);
   }
   if (B * Lq == 0) return DX_OK;
-  const Plan p = make_plan(B, Lq, Lk, H, D, cache_len, cache_lens);
-  DX_CHECK_ARG(p.items < (int64_t(1) << 31), "attention: grid too large");
-  if (p.ws_bytes > 0 && from_scratch) {
-    if (p.ws_bytes > kScratchBytes) {
+  Plan p{};
+  AnyPlan pa{};
+  int64_t need;
+  if (!general) {
+    p = make_plan(B, Lq, Lk, H, D, cache_len, cache_lens);
+    DX_CHECK_ARG(p.items < (int64_t(1) << 31), "attention: grid too large");
+    need = p.ws_bytes;
+  } else {
+    // The workspace query takes no dtype: at head dims 64 and 128 it reports
+    // the 16-bit kernels' bytes, and fp32 calls split no more than fits them.
+    const int64_t cap =
+        D == 64 || D == 128 ? make_plan(B, Lq, Lk, H, D, cache_len, cache_lens).ws_bytes : -1;
+    pa = plan_any(B, Lq, Lk, H, D, max_cache, cap, device_cus());
+    DX_CHECK_ARG(pa.items < (int64_t(1) << 31), "attention: grid too large");
+    need = pa.ws_bytes;
+  }
+  if (need > 0 && from_scratch) {
+    if (need > kScratchBytes) {
       set_error("attention (no-alloc): this call needs %lld bytes of workspace, more than the "
                 "%lld-byte static scratch; use dx_blockwise_causal_attention with a workspace",
-                (long long)p.ws_bytes, (long long)kScratchBytes);
+                (long long)need, (long long)kScratchBytes);
       return DX_EWORKSPACE;
     }
     const int rc = scratch_on_device(&workspace, static_cast<hipStream_t>(stream));
     if (rc != DX_OK) return rc;
     ws_bytes = kScratchBytes;
   }
-  if (p.ws_bytes > 0) {
-    if (!workspace || ws_bytes < p.ws_bytes) {
-      set_error("attention: workspace of %lld bytes needed, %lld given",
-                (long long)p.ws_bytes, (long long)ws_bytes);
+  if (need > 0) {
+    if (!workspace || ws_bytes < need) {
+      set_error("attention: workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)ws_bytes);
       return DX_EWORKSPACE;
     }
     DX_CHECK_ARG(al16(workspace), "attention: workspace must be 16-byte aligned");
+  }
+  if (general) {
+    AttnArgs a{};
+    a.q = static_cast<const uint16_t*>(q); a.q_sb = q_sb; a.q_sl = q_sl; a.q_sh = q_sh;
+    a.k = static_cast<const uint16_t*>(k); a.k_sb = k_sb; a.k_sl = k_sl; a.k_sh = k_sh;
+    a.v = static_cast<const uint16_t*>(v); a.v_sb = v_sb; a.v_sl = v_sl; a.v_sh = v_sh;
+    a.ck = static_cast<const uint16_t*>(cache);
+    a.cv = cache ? reinterpret_cast<const uint16_t*>(static_cast<const char*>(cache) +
+                                                     c_plane * es)
+                 : nullptr;
+    a.c_sb = c_sb; a.c_ss = c_ss; a.c_sh = c_sh;
+    a.out = static_cast<uint16_t*>(out); a.o_sb = o_sb; a.o_sl = o_sl; a.o_sh = o_sh;
+    // Partials after the counter region, which this kernel never writes:
+    // [items * 64 rows][D] fp32 values, then [items * 64 rows] {m, l}.
+    char* ws = static_cast<char*>(workspace);
+    a.ws_o = need ? reinterpret_cast<uint16_t*>(ws + kCounterRegion) : nullptr;
+    a.ws_ml = need ? reinterpret_cast<float*>(ws + kCounterRegion + pa.items * 64 * D * 4)
+                   : nullptr;
+    a.starts = starts; a.starts_i64 = starts_dtype == DX_I64; a.n_blocks = int(n_blocks);
+    a.B = int(B); a.H = int(H); a.Lq = int(Lq); a.Lk = int(Lk);
+    a.kv_group = int(H / Hkv);
+    a.causal = causal != 0;
+    a.n_qtiles = pa.n_qtiles;
+    a.n_splits = pa.splits;
+    // Signed: the kernel masks by selection after the product, so a negative
+    // or zero scale needs no special form.
+    a.scale_log2 = softmax_scale * 1.4426950408889634f;
+    a.cache_len = int(cache_len);
+    a.cache_len_dev = cache_len_dev;
+    a.n_seg = cache_lens ? int(B) : 0;
+    for (int64_t i = 0; cache_lens && i < B; ++i) a.seg_cache[i] = int(cache_lens[i]);
+    const hipError_t e = launch_any(a, dtype, int(D), pa, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      set_error("attention: launch failed: %s", hipGetErrorString(e));
+      return DX_ELAUNCH;
+    }
+    return DX_OK;
   }
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q); a.q_sb = q_sb; a.q_sl = q_sl; a.q_sh = q_sh;
@@ -3902,19 +3803,28 @@ extern "C" int dx_blockwise_causal_attention_varlen(
 extern "C" int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,
                                                 int64_t D, int64_t cache_len,
                                                 const int64_t* cache_lens) {
-  if (B < 0 || Lq < 0 || Lk < 0 || H <= 0 || (D != 64 && D != 128) || cache_len < 0 ||
+  if (B < 0 || Lq < 0 || Lk < 0 || H <= 0 || !any_head_dim(D) || cache_len < 0 ||
       (cache_lens && B > kMaxSeg)) {
     set_error("attention_workspace_bytes: bad shape");
     return -DX_EINVAL;
   }
-  if (cache_lens)
-    for (int64_t i = 0; i < B; ++i)
+  int64_t max_cache = cache_len;
+  if (cache_lens) {
+    max_cache = 0;
+    for (int64_t i = 0; i < B; ++i) {
       if (cache_lens[i] < 0) {
         set_error("attention_workspace_bytes: negative cache length");
         return -DX_EINVAL;
       }
+      max_cache = std::max(max_cache, cache_lens[i]);
+    }
+  }
   if (B * Lq == 0) return 0;
-  return make_plan(B, Lq, Lk, H, D, cache_len, cache_lens).ws_bytes;
+  // Head dims 64 and 128: the 16-bit kernels' plan (an fp32 call of that
+  // shape fits its partials in the same bytes); the others: the general
+  // kernel's, whatever the dtype.
+  if (D == 64 || D == 128) return make_plan(B, Lq, Lk, H, D, cache_len, cache_lens).ws_bytes;
+  return plan_any(B, Lq, Lk, H, D, max_cache, -1, device_cus()).ws_bytes;
 }
 
 #ifdef DX_TIMELINE

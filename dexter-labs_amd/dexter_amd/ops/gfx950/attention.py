@@ -32,6 +32,13 @@ Two cases the reference op cannot take are defined as its callers use them:
   what ``repeat_interleave(H // Hkv, dim=2)`` gives
   (``vla/groot/backbone.py:109-114``), without materialising the copy.
 
+Inputs in bf16 or f16 at head dim 64 or 128 run on the bf16/f16 MFMA kernels;
+fp32 inputs (any supported head dim) and bf16/f16 at head dims 16, 32 and 256
+run on the general kernel (fp32 MFMA, fp32 softmax; ``csrc/attn_any.hip``), as
+the reference op is dtype-generic (``ops/reference/attention.py:62-77``) and
+the Triton kernel takes any power-of-two head dim
+(``blockwise_causal.py:162-172``).
+
 ``cache_len`` may be a device cursor (one int32 on the device,
 ``dx_blockwise_causal_attention_dev``): the kernels read the cached row count
 when they run, clamped to the cache capacity, and the launch is planned for the
@@ -46,14 +53,18 @@ import torch
 
 from ...registry import Priority, register
 from . import _lib
-from ._common import CDNA4, MATRIX_DTYPES, as_rows, device_cursor, strides
+from ._common import CDNA4, as_rows, device_cursor, strides
+
+# Input dtypes and head dims the kernels are built for (the C ABI's own checks).
+ATTN_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+ATTN_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
 def _accepts(q, k, v, *args, **kwargs) -> bool:
-    return (q.is_cuda and q.dtype in MATRIX_DTYPES and q.dim() == 4
+    return (q.is_cuda and q.dtype in ATTN_DTYPES and q.dim() == 4
             and k.dtype == q.dtype and v.dtype == q.dtype
             and k.shape == v.shape and k.dim() == 4
-            and q.shape[-1] in (64, 128) and k.shape[-1] == q.shape[-1]
+            and q.shape[-1] in ATTN_HEAD_DIMS and k.shape[-1] == q.shape[-1]
             and k.shape[2] > 0 and q.shape[2] % k.shape[2] == 0)
 
 
@@ -81,8 +92,9 @@ def _check_cache(kv_cache, b, heads, dim, dtype, need_rows: int):
         raise ValueError(f"kv_cache dtype {kv_cache.dtype} differs from q's {dtype}")
     if kv_cache.shape[2] < need_rows:
         raise ValueError(f"cache_len {need_rows} exceeds the cache capacity {kv_cache.shape[2]}")
+    per16 = 16 // kv_cache.element_size()
     if not (kv_cache.stride(-1) == 1 and kv_cache.data_ptr() % 16 == 0
-            and all(x % 8 == 0 for x in kv_cache.stride()[:-1])):
+            and all(x % per16 == 0 for x in kv_cache.stride()[:-1])):
         raise ValueError("kv_cache must have a contiguous, 16-byte aligned head_dim")
 
 

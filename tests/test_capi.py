@@ -171,3 +171,34 @@ def test_planner_choices_at_the_measured_shapes(built_lib):
     assert lib.dx_attention_workspace_bytes(4, 99, 99, 24, d, 0, lens) == ws(24 * (1 + 1 + 2 + 6), 128)
     assert lib.dx_attention_workspace_bytes(1, 83, 257, 24, d, 0, None) == ws(24 * 5, 128)
     assert lib.dx_attention_workspace_bytes(1, 83, 512, 24, d, 0, None) == ws(24 * 4, 128)
+
+
+def test_general_kernel_plan(built_lib):
+    """fp32 inputs and head dims 16, 32, 256 run on the general kernel, whose
+    workspace is the counter region (never written by it) and then, per split
+    of each 64-query item, 64 rows of D fp32 values and an 8-byte {m, l}
+    record. About two items per CU (256 CUs without a GPU), at least two
+    32-key tiles per split; none when the items alone fill the chip. The
+    workspace query takes no dtype: at head dims 64 and 128 it reports the
+    16-bit kernels' bytes, within which fp32 calls lower their split count."""
+    lib = _lib.load()
+    counters = 256 << 10
+
+    def ws(items, d):
+        return counters + items * 64 * (4 * d + 8)
+
+    # 83 queries x 24 heads: 48 items, 512 // 48 = 10 splits over 42 tiles.
+    assert lib.dx_attention_workspace_bytes(1, 83, 83, 24, 256, 1245, None) == ws(48 * 10, 256)
+    assert lib.dx_attention_workspace_bytes(1, 83, 83, 24, 32, 1245, None) == ws(48 * 10, 32)
+    # Few keys: at most one split per two tiles (40 keys: 2 tiles, 1 split).
+    assert lib.dx_attention_workspace_bytes(1, 20, 20, 2, 16, 20, None) == 0
+    # 3,072 items: no split.
+    assert lib.dx_attention_workspace_bytes(1, 8192, 8192, 24, 32, 0, None) == 0
+    lens = (ctypes.c_int64 * 2)(100, 3000)
+    assert lib.dx_attention_workspace_bytes(2, 16, 16, 4, 256, 0, lens) == ws(8 * 16, 256)
+    assert lib.dx_attention_workspace_bytes(1, 8, 8, 2, 96, 0, None) < 0
+    # Dtype codes other than bf16, f16 and f32 are refused before any launch.
+    args = [16, 0, 0, 0] * 3 + [None, 0, 0, 0, 0] + [16, 0, 0, 0]
+    rc = lib.dx_blockwise_causal_attention(*args, 7, 1, 8, 8, 2, 2, 64, 0, None,
+                                           _lib.DX_I32, 0, 0, 1.0, None, 0, None)
+    assert rc == _lib.DX_EINVAL and "dtype code 7" in lib.dx_last_error().decode()
