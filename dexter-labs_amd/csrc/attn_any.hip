@@ -161,16 +161,19 @@ __global__ __launch_bounds__(kAnyThreads) void attn_any_kernel(AttnArgs a) {
   const int key_end = min(t_end * kAnyKeys, item_end);  // rows loaded: [t_begin * 32, key_end)
   const int lim = min(row_end, key_end);                // this lane's query sees keys < lim
 
-  // q, pre-scaled: qr[u][j] = q[qi, 16 u + 4 g + j] * scale * log2(e).
+  // q, pre-scaled: qr[u][j] = q[qi, 16 u + 4 g + j] * scale * log2(e). Rows
+  // past Lq read the last row and become zeros: loads with no branch between
+  // them all go out before the first wait.
   f32x4 qr[DG];
   {
+    const int qr_i = min(qi, a.Lq - 1);
     const char* qrow = reinterpret_cast<const char*>(a.q) +
-                       (int64_t(b) * a.q_sb + int64_t(qi) * a.q_sl + int64_t(h) * a.q_sh) * es;
+                       (int64_t(b) * a.q_sb + int64_t(qr_i) * a.q_sl + int64_t(h) * a.q_sh) * es;
 #pragma unroll
-    for (int u = 0; u < DG; ++u) {
-      qr[u] = qvalid ? E::load4(qrow + (16 * u + 4 * g) * es) : f32x4{0.f, 0.f, 0.f, 0.f};
-      qr[u] *= a.scale_log2;
-    }
+    for (int u = 0; u < DG; ++u) qr[u] = E::load4(qrow + (16 * u + 4 * g) * es);
+    const float qs = qvalid ? a.scale_log2 : 0.f;
+#pragma unroll
+    for (int u = 0; u < DG; ++u) qr[u] *= qs;
   }
 
   // This thread's chunks of a tile: chunk tid + 256 i is row ci / CPR,
@@ -319,8 +322,10 @@ __global__ __launch_bounds__(kAnyThreads) void attn_any_kernel(AttnArgs a) {
 // Merge of the key splits: row (b, h, query) takes the S partials of its
 // item group, M = max m_s, weights 2^(m_s - M) (0 for a split that saw no key),
 // out = sum w_s acc_s / sum w_s l_s, rounded once to T. D / 4 threads per
-// row, four head-dim elements each.
-template <int D, typename T>
+// row, four head-dim elements each. Instantiated for at most NMAX splits, so
+// that every split's loads go out before the first is used (slots past S read
+// split S - 1 again and weigh nothing).
+template <int D, typename T, int NMAX>
 __global__ __launch_bounds__(kMergeThreads) void attn_any_merge_kernel(AttnArgs a) {
   using E = Elem<T>;
   constexpr int TPR = D / 4;
@@ -337,18 +342,26 @@ __global__ __launch_bounds__(kMergeThreads) void attn_any_merge_kernel(AttnArgs 
   const int qi = qt * kAnyRows + r;
   if (qi >= a.Lq) return;
   const int S = a.n_splits;
+  const float* po = reinterpret_cast<const float*>(a.ws_o);
+  f32x2 ml[NMAX];
+  f32x4 val[NMAX];
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    const int64_t pr = (grp * S + min(s, S - 1)) * kAnyRows + r;
+    ml[s] = *reinterpret_cast<const f32x2*>(a.ws_ml + 2 * pr);
+    val[s] = *reinterpret_cast<const f32x4*>(po + pr * D + 4 * dq);
+  }
   const float kNegInf = -__builtin_inff();
   float mx = kNegInf;
-  for (int s = 0; s < S; ++s) mx = fmaxf(mx, a.ws_ml[2 * ((grp * S + s) * kAnyRows + r)]);
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) mx = fmaxf(mx, ml[s][0]);
   float L = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const float* po = reinterpret_cast<const float*>(a.ws_o);
-  for (int s = 0; s < S; ++s) {
-    const int64_t pr = (grp * S + s) * kAnyRows + r;
-    const f32x2 ml = *reinterpret_cast<const f32x2*>(a.ws_ml + 2 * pr);
-    const float w = mx == kNegInf ? 0.f : __builtin_amdgcn_exp2f(ml[0] - mx);
-    L += w * ml[1];
-    acc += w * *reinterpret_cast<const f32x4*>(po + pr * D + 4 * dq);
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    const float w = mx == kNegInf || s >= S ? 0.f : __builtin_amdgcn_exp2f(ml[s][0] - mx);
+    L += w * ml[s][1];
+    acc += w * val[s];
   }
   char* orow = reinterpret_cast<char*>(a.out) +
                (int64_t(b) * a.o_sb + int64_t(qi) * a.o_sl + int64_t(h) * a.o_sh) * es;
@@ -364,8 +377,14 @@ hipError_t launch_any_dt(const AttnArgs& a, const AnyPlan& p, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int64_t threads = int64_t(a.B) * a.H * p.n_qtiles * kAnyRows * (D / 4);
-  hipLaunchKernelGGL((attn_any_merge_kernel<D, T>), dim3(unsigned(cdiv64(threads, kMergeThreads))),
-                     dim3(kMergeThreads), 0, st, a);
+  const dim3 grid(unsigned(cdiv64(threads, kMergeThreads)));
+  if (p.splits <= 4)
+    hipLaunchKernelGGL((attn_any_merge_kernel<D, T, 4>), grid, dim3(kMergeThreads), 0, st, a);
+  else if (p.splits <= 8)
+    hipLaunchKernelGGL((attn_any_merge_kernel<D, T, 8>), grid, dim3(kMergeThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_any_merge_kernel<D, T, kMaxSplits>), grid, dim3(kMergeThreads), 0,
+                       st, a);
   return hipGetLastError();
 }
 

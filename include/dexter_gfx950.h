@@ -199,8 +199,11 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  * non-negative starts (the reference builds them with torch.arange) let the
  * kernels skip whole future tiles, any other list is masked key by key.
  * softmax_scale multiplies q.k before the softmax (the reference's default
- * is 1/sqrt(D); callers pass it explicitly). dtype: DX_BF16 or DX_F16;
- * D: 64 or 128.
+ * is 1/sqrt(D); callers pass it explicitly). dtype: DX_BF16, DX_F16 or DX_F32
+ * (q, k, v, the cache and out all of it); D: 16, 32, 64, 128 or 256. bf16/f16
+ * at D 64 or 128 run on the 16-bit MFMA kernels; fp32 (any D) and bf16/f16 at
+ * D 16, 32 or 256 on the general kernel (fp32 products and softmax, one
+ * rounding to dtype). Strides are multiples of 16 bytes.
  * out may be strided like q. cache may be NULL when cache_len == 0.
  * workspace must hold dx_attention_workspace_bytes(...) bytes for the same
  * shape (it may be NULL when that is 0). Its first 256 KiB hold the
@@ -345,6 +348,9 @@ int dx_qk_norm_rope_append_dev(const void* q, int64_t q_sb, int64_t q_sl, int64_
  * current device (split-KV partial results); 0 when the launch does not split.
  * Pass cache_len and cache_lens = NULL for dx_blockwise_causal_attention, or
  * the same cache_lens array (cache_len ignored) for the varlen entry point.
+ * It takes no dtype: the bytes cover every dtype of the shape (at D 64 and
+ * 128 an fp32 call splits its keys no further than fits the bf16/f16 plan's
+ * bytes). The general kernel never writes the first 256 KiB (the counters).
  * Returns a negative DX_E* code on a bad shape.
  */
 int64_t dx_attention_workspace_bytes(int64_t B, int64_t Lq, int64_t Lk, int64_t H,

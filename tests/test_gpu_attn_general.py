@@ -89,15 +89,16 @@ def test_c1_shape_fp32(device, built_lib, splits):
 
 
 MODES = ["cache", "causal", "blocks", "blocks_any", "cross"]
+# (dtype, head dim) pairs the general kernel runs: fp32 at any head dim, 16-bit
+# types at those the MFMA kernels do not take.
+GENERAL = [(dt, d) for dt in (torch.float32, torch.bfloat16, torch.float16)
+           for d in (16, 32, 64, 256) if dt == torch.float32 or d != 64]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
-                         ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("d", [16, 32, 64, 256])
+@pytest.mark.parametrize("dtype,d", GENERAL,
+                         ids=[f"{str(dt)[6:]}-D{d}" for dt, d in GENERAL])
 @pytest.mark.parametrize("mode", MODES)
 def test_head_dims_dtypes_masks(device, built_lib, dtype, d, mode):
-    if d == 64 and dtype != torch.float32:
-        pytest.skip("bf16/f16 at head dim 64 run on the MFMA kernels (their own tests)")
     b, lq, h = 2, 77, 4
     lk = 130 if mode == "cross" else lq
     cache_len = 0 if mode in ("causal", "cross") else 200

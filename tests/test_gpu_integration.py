@@ -152,3 +152,29 @@ def test_outgrown_workspace_stays_valid_for_captured_graphs(device, built_lib):
                 big()
             torch.cuda.synchronize()
             assert torch.equal(got, want), f"replay {rep} of the first graph differs"
+
+
+def test_integration_binding_in_fp32_and_at_head_dim_256(device, built_lib):
+    """The same binding with fp32 inputs (C0, the reference's own fp32 case, and
+    a decode chunk over a cache that splits its keys) and with bf16 at head
+    dim 256: the general kernel behind the same entry point."""
+    ns = _load_binding()
+    from dexter_amd.bench.workloads import CONFIGS, make_inputs
+    cfg = CONFIGS["C0"]
+    inp = make_inputs(cfg)
+    bb = torch.tensor(cfg.block_starts)
+    got = ns["attention"](inp.q.to(device), inp.k.to(device), inp.v.to(device), None, 0,
+                          bb.to(device), None)
+    ref = oatt.blockwise_causal_attention(inp.q, inp.k, inp.v, None, 0, bb, None, keep_fp32=True)
+    assert got.dtype == torch.float32
+    assert_parity(got, ref, 1e-4, 1e-5, what="binding, C0 fp32")
+    for dt, d, c in ((torch.float32, 128, 1245), (torch.bfloat16, 256, 700)):
+        g = torch.Generator().manual_seed(d)
+        q, k, v = (torch.randn((1, 83, 4, d), generator=g).to(dt) for _ in range(3))
+        cache = torch.randn((2, 1, c + 83, 4, d), generator=g).to(dt)
+        got = ns["attention"](q.to(device), k.to(device), v.to(device), cache.to(device), c,
+                              None, None)
+        torch.cuda.synchronize()
+        ref = oatt.blockwise_causal_attention(q, k, v, cache, c, None, None, keep_fp32=True)
+        bar = (1e-4, 1e-5) if dt == torch.float32 else (2e-2, 2e-3)
+        assert_parity(got, ref, *bar, what=f"binding, {dt} D={d}")
