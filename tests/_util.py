@@ -10,6 +10,13 @@ MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
 
 
+def report(what: str, text: str) -> None:
+    """One line per named check, shown by ``pytest -s``: the measured errors
+    behind each parity figure, not only whether the bar held."""
+    if what:
+        print(f"[parity] {what}: {text}")
+
+
 def errors(got: torch.Tensor, ref: torch.Tensor) -> tuple[float, float]:
     d = (got.detach().float().cpu() - ref.detach().float().cpu()).abs()
     return d.max().item(), d.mean().item()
@@ -20,6 +27,7 @@ def assert_parity(got, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=""):
     g, r = got.detach().float().cpu(), ref.detach().float().cpu()
     assert torch.isfinite(g).all(), f"{what}: non-finite output"
     mx, mn = errors(g, r)
+    report(what, f"max-abs {mx:.3e} mean-abs {mn:.3e}")
     assert mx <= max_abs and mn <= mean_abs, (
         f"{what}: max-abs {mx:.3e} (<= {max_abs}), mean-abs {mn:.3e} (<= {mean_abs})")
     return mx, mn
@@ -43,6 +51,7 @@ def assert_parity_scaled(got, ref, max_rel=MAX_ABS, mean_abs=MEAN_ABS, what=""):
     assert g.shape == r.shape and torch.isfinite(g).all(), what
     d = (g - r).abs()
     scaled = (d / r.abs().clamp_min(1.0)).max().item()
+    report(what, f"max-abs {d.max().item():.3e} (scaled {scaled:.3e}) mean-abs {d.mean().item():.3e}")
     assert scaled <= max_rel and d.mean().item() <= mean_abs, (
         f"{what}: max-abs {d.max().item():.3e} at scaled {scaled:.3e} (<= {max_rel}), "
         f"mean-abs {d.mean().item():.3e} (<= {mean_abs}), max |ref| {r.abs().max().item():.1f}")
@@ -78,6 +87,7 @@ def assert_within_ulp(got, ref, ulps=1, frac=0.999, min_abs=1.0, mean_abs=MEAN_A
     sel = r16.float().abs() >= min_abs
     within = (n_ulp[sel] <= ulps).float().mean().item() if sel.any() else 1.0
     mn = (g.float() - r).abs().mean().item()
+    report(what, f"{within:.5f} of |ref| >= {min_abs} within {ulps} bf16 ulp")
     assert within >= frac and mn <= mean_abs, (
         f"{what}: {within:.5f} of {int(sel.sum())} elements with |ref| >= {min_abs} within "
         f"{ulps} bf16 ulp (>= {frac}), max {n_ulp[sel].max().item():.1f} ulp there, "
