@@ -27,7 +27,8 @@ struct AttnArgs {
   const uint16_t* v; int64_t v_sb, v_sl, v_sh;
   const uint16_t* ck; const uint16_t* cv; int64_t c_sb, c_ss, c_sh;
   uint16_t* out; int64_t o_sb, o_sl, o_sh;
-  uint16_t* ws_o;  // [partials][bm][D] f16 partial outputs acc / l scaled by 2^-e
+  uint16_t* ws_o;  // [partials][bm x D] f16 partial outputs acc / l scaled by 2^-e (row-major,
+                   // or blocked: unit_off in attn_fwd.hip)
   float* ws_ml;    // [partials][bm][4] {exponent reference m (log2 units), sum l, scale exponent e, 0}
   const void* starts; int starts_i64; int n_blocks;
   int B, H, Lq, Lk;

@@ -1105,6 +1105,19 @@ constexpr int kPMergeSplits = 8;
 // past this CU's L1 to the XCD's L2, which holds every such store.
 constexpr int kScXcd = 1;
 
+// Where a partial keeps its 16-byte unit (row r, chunk ch of 8 head-dim
+// values), in bytes from the partial's start. Row-major: (r CR + ch) 16, CR =
+// D / 8. Blocked (BLK): ((r / 32) CR + ch) 512 + (r % 32) 16, the layout of a
+// wave's MFMA registers, in which the dual-stream kernel stores a partial
+// that the merge kernel will read: a wave stores each (32-row block, chunk)
+// piece as 512 contiguous bytes straight from its registers.
+template <int D, bool BLK>
+__device__ __forceinline__ uint32_t unit_off(int r, int ch) {
+  constexpr uint32_t CR = D / 8;
+  return BLK ? ((uint32_t(r) >> 5) * CR + uint32_t(ch)) * 512u + (uint32_t(r) & 31u) * 16u
+             : (uint32_t(r) * CR + uint32_t(ch)) * 16u;
+}
+
 // The merge, by the last split: thread t < nrows turns row t's records into
 // the split weights (into LDS) while every thread's loads of its units (row,
 // 8 dims: 16 bytes) of the first splits are in flight; then each thread adds
@@ -1462,14 +1475,17 @@ __device__ __forceinline__ void spread_split_group(const AttnArgs& a, const Coor
 // head_dim blocks [s DT / 2, (s + 1) DT / 2) of its wave's 32 rows (r0 ..)
 // and the whole row's (l_tot, mref). Both streams pack their blocks into the
 // row area at ``area``; after a workgroup barrier each stores 16 of the 32
-// rows, whole. A split partial takes one scale exponent per row (as
-// partial_scale's), from ``rbound``: an upper bound of the row's largest
+// rows, whole (row-major). A split partial takes one scale exponent per row
+// (as partial_scale's), from ``rbound``: an upper bound of the row's largest
 // |value| over both streams' blocks that the hand-over already carried, so no
-// exchange of the combined maxima is needed. Every wave of the workgroup
-// calls it (the barrier); ``active``: the wave has rows below Lq.
+// exchange of the combined maxima is needed. BLOCKED: a split partial goes
+// out blocked (unit_off) from the registers instead, with no row area and no
+// barrier (the merge kernel reads that layout; the in-launch merges read
+// row-major partials). Every wave of the workgroup calls it (the barrier, in
+// a call that takes it); ``active``: the wave has rows below Lq.
 // The stream is a template parameter so that every block index is a constant
 // (a register array indexed at run time would live in scratch memory).
-template <int D, typename T, int stream, int kAux = 0>
+template <int D, typename T, int stream, int kAux = 0, bool BLOCKED = false>
 __device__ __forceinline__ int store_result_halves(const AttnArgs& a, const Coord& it, int q0,
                                                     int r0, int g, int lane, int ltid,
                                                     bool active,
@@ -1491,6 +1507,37 @@ __device__ __forceinline__ int store_result_halves(const AttnArgs& a, const Coor
     const float omax = rbound * inv;
     e = omax > 0.f && omax <= FLT_MAX ? __builtin_amdgcn_frexp_expf(omax) : 0;
     k = __builtin_ldexpf(inv, -e);
+    if (BLOCKED) {
+      // Blocked (unit_off), straight from the registers: for each (block d,
+      // r4), lane n + 32 g holds dims 32 d + 8 r4 + 4 g .. + 3 of row r0 + n,
+      // so the wave's 64 lanes store the piece's 512 bytes in one instruction
+      // (rows at or past Lq go past the buffer's bound: not written). No
+      // staging, no barrier.
+      if (!active) return e;
+      const int64_t pidx = it.pbase + it.split;
+      const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+          a.ws_o + pidx * a.bm * D, (short)0, a.bm * D * 2, kBufWord3);
+      const int n = lane & 31;
+#pragma unroll
+      for (int dd = 0; dd < HB; ++dd)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int d = d0 + dd;
+          u32x2 w;
+          w[0] = Mfma<f16_t>::pack(acc[d][4 * r4] * k, acc[d][4 * r4 + 1] * k);
+          w[1] = Mfma<f16_t>::pack(acc[d][4 * r4 + 2] * k, acc[d][4 * r4 + 3] * k);
+          const uint32_t off =
+              n < nrows ? unit_off<D, true>(row, 4 * d + r4) + 8u * uint32_t(g) : 0x80000000u;
+          __builtin_amdgcn_raw_buffer_store_b64(w, rp, off, 0, kAux);
+        }
+      if (stream == 0 && g == 0 && n < nrows)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{l_tot > 0.f ? mref : -INFINITY, l_tot, float(e), 0.f}),
+            __builtin_amdgcn_make_buffer_rsrc(a.ws_ml + pidx * a.bm * 4, (short)0, a.bm * 16,
+                                              kBufWord3),
+            row * 16, 0, kAux);
+      return e;
+    }
   }
   if (active) {
     // Dims 32 d + 8 r4 + 4 g .. + 3 of row ``row``: half g of chunk 4 d + r4.
@@ -1849,8 +1896,9 @@ __global__ __launch_bounds__(64 * kNW * NS, 2) void attn_fwd_kernel(AttnArgs a) 
       // Result rows through stream 1's tile buffers, past the hand-over area.
       const uint32_t area = lds_addr(smem) + Lds<D>::bytes;
       if (!merge_here) {
-        store_result_halves<D, T, S>(a, it, q0, wave * 32, g, lane, ltid, wave_active, acc,
-                                     l_tot, mref, area, rbound);
+        // The output, or a partial for the merge kernel: blocked.
+        store_result_halves<D, T, S, 0, true>(a, it, q0, wave * 32, g, lane, ltid, wave_active,
+                                              acc, l_tot, mref, area, rbound);
         DX_STAMP(4);
         DX_NOTE(8, uint32_t(it.split) | uint32_t(it.n_splits) << 8 | uint32_t(it.b) << 16);
         DX_STAMP(7);
@@ -3008,10 +3056,55 @@ template <int D> struct CombineShape {
 // n_splits partials return zeros for the rest, with no branch between the
 // loads (a guarded load compiles to a wait on every earlier one). Blocks of
 // one (batch, head) run on the XCD whose L2 holds that head's partials.
-template <int D, typename T, int NMAX>
+template <int D, typename T, int NMAX, bool BLK>
 __global__ __launch_bounds__(kCombineThreads) void attn_combine_kernel(AttnArgs a) {
   DX_MERGE_STAMP(0);
   prefetch_args(a);
+  if constexpr (BLK) {
+    // Blocked partials (unit_off): block k of a group takes 32-row block
+    // k / (D / 16) and chunks 2 (k % (D / 16)) and + 1; lane n + 32 h reads row
+    // n of the block, chunk 2 (k % (D / 16)) + h, so a wave's loads of one
+    // split are 1 KB contiguous. The arithmetic is merge_partials', value by
+    // value.
+    static_assert(kCombineThreads == 64, "one wave per block");
+    constexpr int CP = D / 16;  // chunk pairs per row
+    const Coord cd = locate(a, blockIdx.x, true, a.comb_chunks);
+    const int rb = cd.split / CP, cp = cd.split - rb * CP;
+    const int row = 32 * rb + (int(threadIdx.x) & 31), ch = 2 * cp + (int(threadIdx.x) >> 5);
+    const int qi = cd.qtile * a.bm + row;
+    if (row >= a.bm || qi >= a.Lq) return;
+    const uint32_t rows = uint32_t(a.bm), n = uint32_t(cd.n_splits);
+    const __amdgpu_buffer_rsrc_t rrec = __builtin_amdgcn_make_buffer_rsrc(
+        a.ws_ml + cd.pbase * a.bm * 4, (short)0, int(n * rows * 16), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rval = __builtin_amdgcn_make_buffer_rsrc(
+        a.ws_o + cd.pbase * a.bm * D, (short)0, int(n * rows * D * 2), kBufWord3);
+    f32x4 ml[NMAX];
+    u32x4 o[NMAX];
+#pragma unroll
+    for (int s = 0; s < NMAX; ++s) {
+      ml[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rrec, (uint32_t(s) * rows + uint32_t(row)) * 16, 0, 0));
+      o[s] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rval, uint32_t(s) * rows * (D * 2) + unit_off<D, true>(row, ch), 0, 0));
+    }
+    float c[NMAX];
+    const int emax = merge_weights(ml, cd.n_splits, c);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NMAX; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) merge_add2(acc[2 * e], acc[2 * e + 1], c[s], o[s][e]);
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = Mfma<T>::pack(__builtin_ldexpf(acc[2 * e], emax),
+                           __builtin_ldexpf(acc[2 * e + 1], emax));
+    uint16_t* op = a.out + cd.b * a.o_sb + int64_t(qi) * a.o_sl + cd.h * a.o_sh + 8 * ch;
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(op));
+    DX_MERGE_STAMP(1);
+    return;
+  }
   using CS = CombineShape<D>;
   // Blocks per work-item group: ceil(min(bm, Lq) / RPB), as the host sizes
   // the grid (no block for rows that no query tile has; bm need not be a
@@ -3085,8 +3178,12 @@ struct Plan {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-int64_t combine_bpt(int64_t D, int64_t bm) {
-  return cdiv(bm, D == 128 ? CombineShape<128>::RPB : CombineShape<64>::RPB);
+// Merge-kernel blocks per work-item group (rows: min(bm, Lq)): row-major
+// partials take CombineShape's rows per block; blocked ones (the dual-stream
+// kernel's) a 32-row block and two chunks per block.
+int64_t combine_bpt(int64_t D, int64_t rows, bool blocked) {
+  if (blocked) return cdiv(rows, 32) * (D / 16);
+  return cdiv(rows, D == 128 ? CombineShape<128>::RPB : CombineShape<64>::RPB);
 }
 
 int bm_of(int kernel) { return kernel == kPaired ? kBMPair : kBM; }
@@ -3286,7 +3383,8 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
     p.items = B * per_b * p.uniform_splits;
     p.partials = p.uniform_splits > 1 ? p.items : 0;
     const bool combine = p.kernel != kDecode;
-    p.comb_blocks = p.uniform_splits > 1 && combine ? B * per_b * combine_bpt(D, comb_rows) : 0;
+    p.comb_blocks =
+        p.uniform_splits > 1 && combine ? B * per_b * combine_bpt(D, comb_rows, p.kernel == kDual) : 0;
   } else {
     p.n_seg = int(B);
     p.seg_base.push_back(0);
@@ -3300,7 +3398,7 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
       p.seg_base.push_back(int(p.seg_base.back() + per_b * splits[k]));
       const bool combine = p.kernel != kDecode;
       p.comb_base.push_back(int(p.comb_base.back() + (splits[k] > 1 && combine
-                                                          ? per_b * combine_bpt(D, comb_rows) : 0)));
+                                                          ? per_b * combine_bpt(D, comb_rows, p.kernel == kDual) : 0)));
       any_split = any_split || splits[k] > 1;
     }
     p.items = p.seg_base.back();
@@ -3314,7 +3412,9 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
   // The counters are the in-kernel merge's; the merge kernel needs none.
   p.counter_bytes = has_partials ? kCounterRegion : 0;
   // The decode kernel's partial values are laid out as its MFMA registers
-  // hold them (whole 32-row blocks); the others' are row-major, bm rows.
+  // hold them (whole 32-row blocks of its query group); the others' have bm
+  // rows: blocked (unit_off) from the dual-stream kernel for the merge
+  // kernel, else row-major.
   p.prow = p.kernel == kDecode ? 32 * p.nqw : p.bm;
   p.ws_bytes = has_partials
                    ? kCounterRegion + p.partials * p.prow * (D * 2 + 4 * int64_t(sizeof(float)))
@@ -3405,9 +3505,17 @@ hipError_t launch_d(const AttnArgs& a, const Plan& p, hipStream_t st) {
   for (int sk : p.seg_splits) most = std::max(most, sk);
   const dim3 grid(unsigned(p.comb_blocks));
   const dim3 block(kCombineThreads);
-  if (most <= 4) hipLaunchKernelGGL((attn_combine_kernel<D, T, 4>), grid, block, 0, st, a);
-  else if (most <= 8) hipLaunchKernelGGL((attn_combine_kernel<D, T, 8>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((attn_combine_kernel<D, T, kMaxSplits>), grid, block, 0, st, a);
+  // The dual-stream kernel's partials for the merge kernel are blocked, the
+  // paired kernel's row-major.
+  if (p.kernel == kDual) {
+    if (most <= 4) hipLaunchKernelGGL((attn_combine_kernel<D, T, 4, true>), grid, block, 0, st, a);
+    else if (most <= 8) hipLaunchKernelGGL((attn_combine_kernel<D, T, 8, true>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((attn_combine_kernel<D, T, kMaxSplits, true>), grid, block, 0, st, a);
+  } else {
+    if (most <= 4) hipLaunchKernelGGL((attn_combine_kernel<D, T, 4, false>), grid, block, 0, st, a);
+    else if (most <= 8) hipLaunchKernelGGL((attn_combine_kernel<D, T, 8, false>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((attn_combine_kernel<D, T, kMaxSplits, false>), grid, block, 0, st, a);
+  }
   return hipGetLastError();
 }
 
@@ -3634,7 +3742,7 @@ int attention_entry(const void* q, int64_t q_sb, int64_t q_sl, int64_t q_sh, con
   a.causal = causal != 0;
   a.n_qtiles = p.n_qtiles;
   a.bm = p.bm;
-  a.comb_chunks = int(combine_bpt(D, std::min<int64_t>(p.bm, Lq)));
+  a.comb_chunks = int(combine_bpt(D, std::min<int64_t>(p.bm, Lq), p.kernel == kDual));
   // A negative scale enters as a negated q (exact) and |scale|, so the kernel
   // only ever multiplies scores by a non-negative factor.
   a.negate_q = softmax_scale < 0.f;
