@@ -208,7 +208,8 @@ def run_headline(args, device):
             "frac": achieved / PEAK_HBM_GBPS,
             "traffic": traffic["bytes"] if traffic else None,
             "kernel": ("one attention call at C1 = attn_fwd_kernel<128,bf16_t,2> (split-KV, "
-                       "dual-stream) + attn_combine_kernel<128,bf16_t,8>"),
+                       "dual-stream, partials stored blocked) + "
+                       "attn_combine_kernel<128,bf16_t,8,true>"),
             "profiled": profiled,
             "algorithmic_bytes_per_launch": attn_bytes,
             "launch_us": attn_ms * 1e3,
