@@ -3365,7 +3365,14 @@ Plan make_plan(int64_t B, int64_t Lq, int64_t Lk, int64_t H, int64_t D, int64_t 
         // split rather than leaving one split half the work (Wan-5B chunk:
         // 257 image keys, 5 tiles, 9.98 us in 5 splits against 10.3 us in 3;
         // 512 text keys, 8 tiles, 10.38 us in 4 against 10.54 us in 8).
-        const int64_t most = (3 * cus) / (4 * groups);
+        // Longer ranges, more than four tiles a split at that count, take a
+        // split per CU instead: the tile loop then dominates, and every CU
+        // streaming raises the call's HBM rate (24 heads x 83 queries over 4K,
+        // 16K and 64K cached keys: 18.85 / 46.35 / 148.1 us at 10 splits
+        // against 19.70 / 51.55 / 168.4 us at 8; 12 and 16 splits, past one
+        // workgroup per CU, 26.8 / 68.1 / 218 and 25.4 / 56.8 / 174 us).
+        int64_t most = (3 * cus) / (4 * groups);
+        if (most >= 1 && cdiv(tiles[k], most) > 4) most = std::max<int64_t>(most, cus / groups);
         sk = tiles[k] % 2 == 1 && tiles[k] <= most ? tiles[k]
                                                    : std::min<int64_t>(most, cdiv(tiles[k], 2));
       }
