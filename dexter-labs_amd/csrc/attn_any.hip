@@ -1,8 +1,10 @@
-// The general attention kernel for gfx950: the calls that the 16-bit MFMA
+// The general attention kernels for gfx950: the calls that the 16-bit MFMA
 // kernels (attn_fwd.hip) do not take -- fp32 inputs at any supported head
 // dim, and bf16/f16 inputs at head dims 16, 32 and 256 -- under the same
-// arguments and the same mask rules (attn_common.h), computed in fp32 from
-// end to end. The reference op is dtype-generic (ops/reference/attention.py:
+// arguments and the same mask rules (attn_common.h). attn_any_kernel works in
+// fp32 from end to end (fp32 inputs, and 16-bit inputs at head dim 16);
+// attn_any16_kernel multiplies 16-bit inputs at head dims 32 and 256 on the
+// 16-bit MFMA with fp32 sums (described at its definition). The reference op is dtype-generic (ops/reference/attention.py:
 // 62-77: fp32 logits, softmax and product, one rounding to q's dtype) and the
 // Triton kernel it stands beside takes any power-of-two head dim
 // (ops/gfx1151/attention/blockwise_causal.py:162-172).
@@ -319,6 +321,239 @@ __global__ __launch_bounds__(kAnyThreads) void attn_any_kernel(AttnArgs a) {
   if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * prow) = f32x2{m, lt};
 }
 
+// 16-bit inputs at head dims that are multiples of 32 and that the 16-bit
+// kernels of attn_fwd.hip do not take (32 and 256): the same work items,
+// 32-key tiles, two-stage LDS ring, masks and fp32 partials as
+// attn_any_kernel, with 16-bit MFMA on the values as they are
+// (v_mfma_f32_16x16x32_{bf16,f16}, fp32 sums) and K and V kept 16-bit in LDS.
+//  * S^T = K Q^T: A = K (lane: key 16 s + l % 16, dims 32 ks + 8 g .. + 7),
+//    B = Q^T (lane: query l % 16, the same dims), so the accumulator holds
+//    query l % 16 and keys 16 s + 4 g + r, as in the fp32 form. Scores are
+//    scaled by the signed scale x log2(e) in fp32, then masked by selection.
+//  * O^T += V^T P^T with the MFMA's K index assigned to keys so that lane
+//    group g's eight slots are keys {4 g .. 4 g + 3, 16 + 4 g .. 16 + 4 g + 3}:
+//    B is the lane's own eight probabilities, rounded to T, and A (head_dim
+//    column 16 u + l % 16 at those keys) comes from the row-major V tile by
+//    two transposing reads (ds_read_b64_tr_b16: within each group of 16
+//    lanes, lane i receives element i % 4 of the 8-byte chunks addressed by
+//    lanes 4 e + i / 4, e = 0..3; lane 4 e + t addresses row 4 g + e, or
+//    16 + 4 g + e, at columns 16 u + 4 t .. + 3). l sums the rounded
+//    probabilities, the values the product uses.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16_t> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16_t> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16*)((__attribute__((address_space(3))) uint16_t*)(p)));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+template <int D> struct Any16Lds {
+  static constexpr int RS = D + 8;             // row stride in 16-bit elements
+  static constexpr int tile = kAnyKeys * RS;   // elements per K or V tile
+  static constexpr int bytes = 2 * 2 * tile * 2;
+};
+
+template <int D, typename T>
+__global__ __launch_bounds__(kAnyThreads) void attn_any16_kernel(AttnArgs a) {
+  static_assert(sizeof(T) == 2 && D % 32 == 0, "16-bit inputs, head dim a multiple of 32");
+  constexpr int RS = Any16Lds<D>::RS;
+  constexpr int TILE = Any16Lds<D>::tile;
+  constexpr int CPR = D / 8;                           // 16-byte chunks per key row
+  constexpr int NCH = kAnyKeys * CPR;                  // chunks per tile of K (or V)
+  constexpr int NPT = (NCH + kAnyThreads - 1) / kAnyThreads;
+  constexpr int KS = D / 32;                           // S k-steps
+  constexpr int DG = D / 16;                           // 16-wide head-dim groups
+  constexpr int es = 2;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * TILE];
+
+  const int tid = int(threadIdx.x), wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, c = lane & 15;
+
+  int item = int(blockIdx.x);
+  const int S = a.n_splits;
+  const int split = item % S;
+  item /= S;
+  const int qt = item % a.n_qtiles;
+  item /= a.n_qtiles;
+  const int h = item % a.H, b = item / a.H;
+  const int hk = h / a.kv_group;
+  const int cache_len = any_cache_len(a, b);
+
+  const int q0 = qt * kAnyRows;
+  const int qi = q0 + 16 * wave + c;
+  const bool qvalid = qi < a.Lq;
+  const int row_end = qvalid ? cache_len + visible_end(a, qi, cache_len) : 0;
+  const EndBounds eb = end_bounds(a, q0, min(q0 + kAnyRows, a.Lq) - 1);
+  const int item_end = cache_len + eb.hi;
+  const int n_tiles = (item_end + kAnyKeys - 1) / kAnyKeys;
+  const int per_split = (n_tiles + S - 1) / S;
+  const int t_begin = min(split * per_split, n_tiles);
+  const int t_end = min(t_begin + per_split, n_tiles);
+  const int key_end = min(t_end * kAnyKeys, item_end);
+  const int lim = min(row_end, key_end);
+
+  // Q^T operand per k-step: q[qi, 32 ks + 8 g .. + 7] (zeros past Lq: the
+  // last row's loads, then masked, so no branch sits between the loads).
+  u32x4 qb[KS];
+  {
+    const int qr_i = min(qi, a.Lq - 1);
+    const char* qrow = reinterpret_cast<const char*>(a.q) +
+                       (int64_t(b) * a.q_sb + int64_t(qr_i) * a.q_sl + int64_t(h) * a.q_sh) * es;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qb[ks] = *reinterpret_cast<const u32x4*>(qrow + (32 * ks + 8 * g) * es);
+    const uint32_t qmask = qvalid ? ~0u : 0u;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qb[ks] &= qmask;
+  }
+  const float cs = a.scale_log2;  // signed: masking selects after the product
+
+  const char* kc = reinterpret_cast<const char*>(a.ck);
+  const char* vc = reinterpret_cast<const char*>(a.cv);
+  const char* kn = reinterpret_cast<const char*>(a.k);
+  const char* vn = reinterpret_cast<const char*>(a.v);
+  u32x4 kreg[NPT], vreg[NPT];
+  auto load_tile = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const int ci = tid + kAnyThreads * i;
+      const int r = ci / CPR, cc = ci % CPR;
+      const int j = t * kAnyKeys + r;
+      kreg[i] = u32x4{0u, 0u, 0u, 0u};
+      vreg[i] = u32x4{0u, 0u, 0u, 0u};
+      if ((NCH % kAnyThreads == 0 || ci < NCH) && j < key_end) {
+        int64_t ko, vo;
+        const char *kb, *vb;
+        if (j < cache_len) {
+          ko = (int64_t(b) * a.c_sb + int64_t(j) * a.c_ss + int64_t(hk) * a.c_sh) * es;
+          vo = ko;
+          kb = kc;
+          vb = vc;
+        } else {
+          const int64_t jn = j - cache_len;
+          ko = (int64_t(b) * a.k_sb + jn * a.k_sl + int64_t(hk) * a.k_sh) * es;
+          vo = (int64_t(b) * a.v_sb + jn * a.v_sl + int64_t(hk) * a.v_sh) * es;
+          kb = kn;
+          vb = vn;
+        }
+        kreg[i] = *reinterpret_cast<const u32x4*>(kb + ko + 16 * cc);
+        vreg[i] = *reinterpret_cast<const u32x4*>(vb + vo + 16 * cc);
+      }
+    }
+  };
+  auto store_tile = [&](int stage) __attribute__((always_inline)) {
+    uint16_t* kt = lds + stage * 2 * TILE;
+    uint16_t* vt = kt + TILE;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const int ci = tid + kAnyThreads * i;
+      if (NCH % kAnyThreads == 0 || ci < NCH) {
+        const int r = ci / CPR, cc = ci % CPR;
+        *reinterpret_cast<u32x4*>(kt + r * RS + 8 * cc) = kreg[i];
+        *reinterpret_cast<u32x4*>(vt + r * RS + 8 * cc) = vreg[i];
+      }
+    }
+  };
+
+  const float kNegInf = -__builtin_inff();
+  float m = kNegInf, l = 0.f;
+  f32x4 o[DG];
+#pragma unroll
+  for (int u = 0; u < DG; ++u) o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // This lane's transposing-read offsets (elements) in a V tile: rows 4 g + e
+  // and 16 + 4 g + e, columns 4 t (+ 16 u per head-dim group).
+  const int tr_lo = (4 * g + (c >> 2)) * RS + 4 * (c & 3);
+  const int tr_hi = tr_lo + 16 * RS;
+
+  if (t_begin < t_end) {
+    load_tile(t_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = t_begin; t < t_end; ++t) {
+    const int stage = (t - t_begin) & 1;
+    if (t + 1 < t_end) load_tile(t + 1);
+    const uint16_t* kt = lds + stage * 2 * TILE;
+    const uint16_t* vt = kt + TILE;
+
+    f32x4 sc[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      sc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = kt + (16 * s + c) * RS + 8 * g;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        sc[s] = Mfma16<T>::run(*reinterpret_cast<const u32x4*>(krow + 32 * ks), qb[ks], sc[s]);
+    }
+    float tmax = kNegInf;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = t * kAnyKeys + 16 * s + 4 * g + r;
+        sc[s][r] = key < lim ? sc[s][r] * cs : kNegInf;
+        tmax = fmaxf(tmax, sc[s][r]);
+      }
+    tmax = quad_max(tmax);
+    const float mn = fmaxf(m, tmax);
+    const float ref = mn == kNegInf ? 0.f : mn;  // nothing visible yet: every p is 0
+    const float corr = __builtin_amdgcn_exp2f(m - ref);
+    u32x4 pb;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int w = 0; w < 2; ++w)
+        pb[2 * s + w] = pack2<T>(__builtin_amdgcn_exp2f(sc[s][2 * w] - ref),
+                                 __builtin_amdgcn_exp2f(sc[s][2 * w + 1] - ref));
+    float ps = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      ps += to_f32(T{uint16_t(pb[w] & 0xffffu)}) + to_f32(T{uint16_t(pb[w] >> 16)});
+    l = l * corr + ps;
+    m = mn;
+#pragma unroll
+    for (int u = 0; u < DG; ++u) o[u] *= corr;
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const u32x2 lo = lds_tr16(vt + tr_lo + 16 * u);
+      const u32x2 hi = lds_tr16(vt + tr_hi + 16 * u);
+      o[u] = Mfma16<T>::run(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb, o[u]);
+    }
+    if (t + 1 < t_end) store_tile(stage ^ 1);
+    __syncthreads();
+  }
+
+  const float lt = quad_sum(l);
+  if (!qvalid) return;
+  if (S == 1) {
+    const float inv = 1.f / lt;
+    char* orow = reinterpret_cast<char*>(a.out) +
+                 (int64_t(b) * a.o_sb + int64_t(qi) * a.o_sl + int64_t(h) * a.o_sh) * es;
+#pragma unroll
+    for (int u = 0; u < DG; ++u) Elem<T>::store4(orow + (16 * u + 4 * g) * es, o[u] * inv);
+    return;
+  }
+  const int64_t prow = int64_t(blockIdx.x) * kAnyRows + 16 * wave + c;
+  float* po = reinterpret_cast<float*>(a.ws_o) + prow * D + 4 * g;
+#pragma unroll
+  for (int u = 0; u < DG; ++u) *reinterpret_cast<f32x4*>(po + 16 * u) = o[u];
+  if (g == 0) *reinterpret_cast<f32x2*>(a.ws_ml + 2 * prow) = f32x2{m, lt};
+}
+
 // Merge of the key splits: row (b, h, query) takes the S partials of its
 // item group, M = max m_s, weights 2^(m_s - M) (0 for a split that saw no key),
 // out = sum w_s acc_s / sum w_s l_s, rounded once to T. D / 4 threads per
@@ -372,8 +607,13 @@ int64_t cdiv64(int64_t x, int64_t y) { return (x + y - 1) / y; }
 
 template <int D, typename T>
 hipError_t launch_any_dt(const AttnArgs& a, const AnyPlan& p, hipStream_t st) {
-  hipLaunchKernelGGL((attn_any_kernel<D, T>), dim3(unsigned(p.items)), dim3(kAnyThreads), 0, st,
-                     a);
+  // 16-bit inputs at head dims that are multiples of 32: 16-bit MFMA.
+  if constexpr (sizeof(T) == 2 && D % 32 == 0)
+    hipLaunchKernelGGL((attn_any16_kernel<D, T>), dim3(unsigned(p.items)), dim3(kAnyThreads), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((attn_any_kernel<D, T>), dim3(unsigned(p.items)), dim3(kAnyThreads), 0,
+                       st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int64_t threads = int64_t(a.B) * a.H * p.n_qtiles * kAnyRows * (D / 4);

@@ -202,8 +202,9 @@ int dx_kv_append(const void* k, int64_t k_sb, int64_t k_sl, int64_t k_sh,
  * is 1/sqrt(D); callers pass it explicitly). dtype: DX_BF16, DX_F16 or DX_F32
  * (q, k, v, the cache and out all of it); D: 16, 32, 64, 128 or 256. bf16/f16
  * at D 64 or 128 run on the 16-bit MFMA kernels; fp32 (any D) and bf16/f16 at
- * D 16, 32 or 256 on the general kernel (fp32 products and softmax, one
- * rounding to dtype). Strides are multiples of 16 bytes.
+ * D 16, 32 or 256 on the general kernels (fp32 softmax and sums, products of
+ * the inputs as they are: fp32, or 16-bit MFMA for bf16/f16 at D 32 and 256;
+ * one rounding to dtype). Strides are multiples of 16 bytes.
  * out may be strided like q. cache may be NULL when cache_len == 0.
  * workspace must hold dx_attention_workspace_bytes(...) bytes for the same
  * shape (it may be NULL when that is 0). Its first 256 KiB hold the
