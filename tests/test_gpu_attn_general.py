@@ -4,9 +4,10 @@ The reference op is dtype-generic (``ops/reference/attention.py:62-77``: fp32
 logits, softmax and product, then ``.to(q.dtype)``) and the Triton kernel it
 stands beside takes any power-of-two head dim
 (``ops/gfx1151/attention/blockwise_causal.py:162-172``). Calls the bf16/f16
-MFMA kernels do not take run on ``csrc/attn_any.hip`` (fp32 MFMA, fp32
-softmax); everything goes through the registry and the C ABI and is compared
-with ``oracle/attention.py``.
+MFMA kernels do not take run on ``csrc/attn_any.hip`` (fp32 softmax and sums;
+fp32 MFMA for fp32 inputs and head dim 16, 16-bit MFMA for bf16/f16 at head
+dims 32 and 256); everything goes through the registry and the C ABI and is
+compared with ``oracle/attention.py``.
 
 Parity bars:
 
