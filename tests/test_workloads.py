@@ -36,3 +36,21 @@ def test_inputs_are_seeded_and_shaped():
     assert c4.q.shape == (4, 99, 24, 128) and c4.k.shape == (4, 3336, 24, 128)
     big = (c4.q.float().abs() > 8).float().mean().item()
     assert 0.0005 < big < 0.02  # ~1% of entries scaled x20 (minus those landing small)
+
+
+@pytest.mark.parametrize("argv, env", [(["--gpus", "2"], {}), (["--gpus", "8"], {}),
+                                       ([], {"WORLD_SIZE": "4"})])
+def test_bench_refuses_more_than_one_gpu(argv, env):
+    """bench.py measures one GPU: asked for more, it exits with code 2 and says so, before
+    importing torch or touching a device."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), *argv],
+                          env={**os.environ, **env}, capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 2
+    assert "one GPU only" in proc.stderr
+    assert proc.stdout == ""
